@@ -1,0 +1,96 @@
+// Shared device helpers for the gfx950 kernels: bf16 carriers, wave64
+// reductions, MFMA operand types and the error word.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fh {
+
+// ---- bf16 carriers -------------------------------------------------------
+// Narrowing is round-to-nearest-even on the f32 bit pattern; NaN payloads are
+// quieted by setting bit 6 of the bf16 (0x0040). This is the rule the
+// reference pins in device/qwen3-gemm-v1/tests/reference.rs:3-11 and :112-135
+// (e.g. 0x3f808000 -> 0x3f80, 0x3f818000 -> 0x3f82, 0x7fa10001 -> 0x7fe1).
+
+__host__ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+__host__ __device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu) != 0u) return ((b >> 16) | 0x0040u) & 0xffffu;
+  return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Value after a round trip through bf16 (the reference's intermediate narrowing).
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+__device__ __forceinline__ bool is_finite_f32(float v) {
+  return (__builtin_bit_cast(uint32_t, v) & 0x7f800000u) != 0x7f800000u;
+}
+
+// Low / high bf16 of a packed dword, widened.
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// ---- error word -----------------------------------------------------------
+// Kernels never trap: where the reference traps (nonfinite value, index out of
+// range) they OR a bit into a device word that the host checks after the step.
+enum : uint32_t {
+  ERR_NONFINITE = 1u,
+  ERR_TOKEN = 2u,
+  ERR_POSITION = 4u,
+  ERR_PAGE = 8u,
+};
+
+__device__ __forceinline__ void raise_error(uint32_t* err, uint32_t bit) {
+  if (err) atomicOr(err, bit);
+}
+
+// ---- wave64 reductions (fixed butterfly order: deterministic) -------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ---- MFMA operand types (gfx950 v_mfma_f32_16x16x32_bf16) -----------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Tile order of a projection weight W[n][k] (n % 16 == 0, k % 32 == 0): a
+// 16-row x 32-column tile is 1 KiB, stored as 64 lanes x 16 bytes in the exact
+// order the MFMA A operand wants it (lane = row + 16 * (col / 8), 8 bf16 per
+// lane). Tiles are stored tile-row major: tile (nb, kb) at (nb * KB + kb) KiB.
+__host__ __device__ __forceinline__ uint64_t tiled_offset(uint32_t n, uint32_t k, uint32_t K) {
+  uint32_t kb_count = K >> 5;
+  uint32_t nb = n >> 4, r = n & 15u, kb = k >> 5, kk = k & 31u;
+  uint32_t lane = r + 16u * (kk >> 3);
+  return ((((uint64_t)nb * kb_count + kb) * 64u + lane) << 3) + (kk & 7u);
+}
+
+// SwiGLU element in the stable-sigmoid form of qwen3_swiglu_element_v1
+// (device/qwen3-all-kernels-v1/src/swiglu.rs:62-101): e = exp(-|g|),
+// sigmoid = (g >= 0 ? 1 : e) / (1 + e), y = bf16((g * sigmoid) * u).
+__device__ __forceinline__ uint32_t swiglu_bf16(float g, float u, bool& bad) {
+  bool nonneg = g >= 0.0f;
+  float e = expf(nonneg ? -g : g);
+  float denom = 1.0f + e;
+  float sig = __fdiv_rn(nonneg ? 1.0f : e, denom);
+  float silu = g * sig;
+  float prod = silu * u;
+  uint32_t out = f32_to_bf16(prod);
+  bad |= !is_finite_f32(g) | !is_finite_f32(u) | ((out & 0x7f80u) == 0x7f80u);
+  return out;
+}
+
+}  // namespace fh

@@ -1,0 +1,63 @@
+// Host-side launchers for the gfx950 kernels. Each returns the HIP error of
+// the launch; shapes are validated by the callers (ops.hip / runtime.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fh {
+
+// Attention split size: each partial workgroup covers this many context
+// tokens (16 pages of 16 tokens).
+constexpr uint32_t kAttnSplitTokens = 256;
+// Floats per attention partial record: running max, denominator, numerator[128].
+constexpr uint32_t kAttnPartialFloats = 2 + 128;
+// Argmax first-pass shards per row.
+constexpr uint32_t kArgmaxShards = 64;
+
+inline uint32_t attn_max_splits(uint32_t context_tokens) {
+  return (context_tokens + kAttnSplitTokens - 1) / kAttnSplitTokens;
+}
+
+// layout / data movement
+hipError_t launch_tile_weight(const uint16_t* src, uint16_t* dst, uint32_t n, uint32_t k, uint32_t tile_mul,
+                              uint32_t tile_add, hipStream_t s);
+hipError_t launch_untile_weight(const uint16_t* tiled, uint16_t* dst, uint32_t n, uint32_t k, hipStream_t s);
+hipError_t launch_embedding(const uint32_t* tokens, const uint16_t* table_tiled, uint16_t* out, uint32_t rows,
+                            uint32_t hidden, uint32_t vocab, uint32_t* err, hipStream_t s);
+hipError_t launch_synth_fill(uint16_t* dst, uint64_t count, uint64_t tensor_seed, float scale, hipStream_t s);
+hipError_t launch_fill_u16(uint16_t* dst, uint64_t count, uint16_t value, hipStream_t s);
+hipError_t launch_kv_fill(uint16_t* cache, const uint32_t* table, const uint32_t* lengths, const uint64_t* keys,
+                          uint32_t rows, uint32_t stride, uint32_t kv_heads, uint64_t tensor_seed, float scale,
+                          uint32_t context_stride, uint32_t max_length, hipStream_t s);
+hipError_t launch_clear_word(uint32_t* word, hipStream_t s);
+hipError_t launch_copy_u16(const uint16_t* src, uint16_t* dst, uint64_t count, hipStream_t s);
+
+// norms / activation
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, uint32_t rows, uint32_t width,
+                          float eps, uint32_t* err, hipStream_t s);
+hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                                 const float* cos_t, const float* sin_t, const uint32_t* positions,
+                                 const uint32_t* table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                 uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
+                                 uint32_t context, float eps, uint32_t* err, hipStream_t s);
+hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t n, uint32_t* err,
+                         hipStream_t s);
+
+// projections
+hipError_t launch_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s);
+
+// attention
+hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                    const uint32_t* positions, const uint32_t* table, float* partials, uint32_t rows,
+                                    uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                                    uint32_t* err, hipStream_t s);
+hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out, uint32_t rows,
+                                  uint32_t qh, uint32_t context, uint32_t* err, hipStream_t s);
+
+// logits
+hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
+                         uint32_t* err, hipStream_t s);
+
+}  // namespace fh

@@ -1,0 +1,154 @@
+// C ABI for the individual kernel roots (fh_op_*), scratch sizing, and the
+// integer speculative-decoding helpers. Every entry point validates its
+// shapes on the host before launching, so a kernel never sees a geometry it
+// was not written for.
+#include <cstring>
+
+#include "../../include/ferric_hip.h"
+#include "kernels.hpp"
+
+namespace {
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline fh_status from_hip(hipError_t e) { return e == hipSuccess ? FH_OK : FH_ERR_DEVICE; }
+
+}  // namespace
+
+extern "C" {
+
+fh_status fh_op_tile_weight(const uint16_t* src, uint16_t* dst, uint32_t n, uint32_t k, void* stream) {
+  if (!src || !dst || n == 0 || k == 0 || n % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_tile_weight(src, dst, n, k, 1, 0, as_stream(stream)));
+}
+
+fh_status fh_op_tile_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* dst, uint32_t i, uint32_t k,
+                             void* stream) {
+  if (!gate || !up || !dst || i == 0 || k == 0 || i % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  hipError_t e = fh::launch_tile_weight(gate, dst, i, k, 2, 0, as_stream(stream));
+  if (e == hipSuccess) e = fh::launch_tile_weight(up, dst, i, k, 2, 1, as_stream(stream));
+  return from_hip(e);
+}
+
+fh_status fh_op_untile_weight(const uint16_t* tiled, uint16_t* dst, uint32_t n, uint32_t k, void* stream) {
+  if (!tiled || !dst || n == 0 || k == 0 || n % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_untile_weight(tiled, dst, n, k, as_stream(stream)));
+}
+
+fh_status fh_op_embedding(const uint32_t* tokens, const uint16_t* table_tiled, uint16_t* out, uint32_t rows,
+                          uint32_t hidden, uint32_t vocabulary, uint32_t* error_word, void* stream) {
+  if (!tokens || !table_tiled || !out || rows == 0 || hidden == 0 || hidden % 32 || vocabulary == 0 ||
+      vocabulary % 16)
+    return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_embedding(tokens, table_tiled, out, rows, hidden, vocabulary, error_word,
+                                       as_stream(stream)));
+}
+
+fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, uint32_t rows, uint32_t width,
+                        float epsilon, uint32_t* error_word, void* stream) {
+  if (!x || !weight || !y || rows == 0 || width == 0 || width % 8 || width > 8192) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_rmsnorm(x, weight, y, rows, width, epsilon, error_word, as_stream(stream)));
+}
+
+fh_status fh_op_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                     uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, void* stream) {
+  if (!x || !w_tiled || !out || m == 0 || m > 32 || n == 0 || k == 0 || n % 16 || k % 32 || ldx < k || ldx % 8)
+    return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue > FH_EPI_F32) return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue == FH_EPI_RESIDUAL && !residual) return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue == FH_EPI_SWIGLU) {
+    if (n % 32 || ldo < n / 2) return FH_ERR_INVALID_ARGUMENT;
+  } else if (ldo < n) {
+    return FH_ERR_INVALID_ARGUMENT;
+  }
+  return from_hip(fh::launch_gemm(x, ldx, w_tiled, m, n, k, epilogue, residual, out, ldo, as_stream(stream)));
+}
+
+fh_status fh_op_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                               const float* cos_table, const float* sin_table, const uint32_t* positions,
+                               const uint32_t* page_table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                               uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
+                               uint32_t physical_pages, uint32_t context_tokens, float epsilon, uint32_t* error_word,
+                               void* stream) {
+  if (!qkv || !q_norm || !k_norm || !cos_table || !sin_table || !positions || !page_table || !q_out || !k_cache ||
+      !v_cache || rows == 0 || query_heads == 0 || kv_heads == 0 || query_heads + kv_heads > 64 || stride == 0 ||
+      physical_pages == 0 || context_tokens == 0)
+    return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_qknorm_rope_kv(qkv, q_norm, k_norm, cos_table, sin_table, positions, page_table, q_out,
+                                            k_cache, v_cache, rows, query_heads, kv_heads, stride, physical_pages,
+                                            context_tokens, epsilon, error_word, as_stream(stream)));
+}
+
+uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens) {
+  return (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens) * fh::kAttnPartialFloats * 4;
+}
+
+fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                const uint32_t* positions, const uint32_t* page_table, uint16_t* out, void* scratch,
+                                uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
+                                uint32_t physical_pages, uint32_t context_tokens, uint32_t* error_word,
+                                void* stream) {
+  if (!q || !k_cache || !v_cache || !positions || !page_table || !out || !scratch || rows == 0 || kv_heads == 0 ||
+      query_heads % kv_heads != 0 || stride == 0 || physical_pages == 0 || context_tokens == 0 ||
+      (uint64_t)stride * 16 < context_tokens)
+    return FH_ERR_INVALID_ARGUMENT;
+  const uint32_t g = query_heads / kv_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
+  hipStream_t s = as_stream(stream);
+  float* part = reinterpret_cast<float*>(scratch);
+  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, rows, query_heads,
+                                              kv_heads, stride, physical_pages, context_tokens, error_word, s);
+  if (e == hipSuccess) e = fh::launch_attention_merge(part, positions, out, rows, query_heads, context_tokens,
+                                                      error_word, s);
+  return from_hip(e);
+}
+
+fh_status fh_op_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t elements,
+                       uint32_t* error_word, void* stream) {
+  if (!gate || !up || !out || elements == 0) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_swiglu(gate, up, out, elements, error_word, as_stream(stream)));
+}
+
+uint64_t fh_argmax_scratch_bytes(uint32_t rows) { return (uint64_t)rows * fh::kArgmaxShards * 8; }
+
+fh_status fh_op_argmax(const float* logits, uint32_t rows, uint32_t vocabulary, void* scratch, uint32_t* choices,
+                       uint32_t* error_word, void* stream) {
+  if (!logits || !scratch || !choices || rows == 0 || vocabulary == 0) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_argmax(logits, rows, vocabulary, scratch, choices, error_word, as_stream(stream)));
+}
+
+fh_status fh_op_synth_fill(uint16_t* dst, uint64_t count, uint64_t tensor_seed, float scale, void* stream) {
+  if (!dst || count == 0) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_synth_fill(dst, count, tensor_seed, scale, as_stream(stream)));
+}
+
+// target_ids[s][0] = anchor, target_ids[s][1 + i] = draft[i][s]
+// (ferric_qwen3_speculative_token_assembly_v1, device/qwen3-all-kernels-v1/src/logits.rs:587).
+fh_status fh_speculative_token_assembly(const uint32_t* anchors, const uint32_t* draft, uint32_t sequences,
+                                        uint32_t k, uint32_t* target_ids) {
+  if (!anchors || (k && !draft) || !target_ids || sequences == 0) return FH_ERR_INVALID_ARGUMENT;
+  for (uint32_t s = 0; s < sequences; ++s) {
+    target_ids[(uint64_t)s * (k + 1)] = anchors[s];
+    for (uint32_t i = 0; i < k; ++i) target_ids[(uint64_t)s * (k + 1) + 1 + i] = draft[(uint64_t)i * sequences + s];
+  }
+  return FH_OK;
+}
+
+// Greedy speculative verification (crates/ferric-spec/src/speculation.rs:126-200).
+fh_status fh_verify_greedy_round(const uint32_t* draft, uint32_t draft_count, const uint32_t* target,
+                                 uint32_t target_count, uint32_t* accepted, uint32_t* emitted,
+                                 uint32_t* emitted_count) {
+  if (!target || !accepted || !emitted || !emitted_count || (draft_count && !draft)) return FH_ERR_INVALID_ARGUMENT;
+  if (target_count == 0) return FH_ERR_INVALID_ARGUMENT;                  // MissingTargetBonus
+  if (draft_count == 0xffffffffu) return FH_ERR_INVALID_ARGUMENT;         // DraftTokenCountOverflow
+  if (target_count != draft_count + 1) return FH_ERR_INVALID_ARGUMENT;    // IncorrectTargetChoiceCount
+  uint32_t a = 0;
+  while (a < draft_count && draft[a] == target[a]) ++a;
+  for (uint32_t i = 0; i < a; ++i) emitted[i] = draft[i];
+  emitted[a] = target[a];
+  *accepted = a;
+  *emitted_count = a + 1;
+  return FH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,823 @@
+// Host runtime behind the C ABI: the resident model (weights in MFMA tile
+// order), the paged KV pool, per-step metadata, and fh_execute_batch — the
+// replacement for EngineeringTpBatchExecutionV2::forward
+// (adapters/m1-engineering-execution-v1/src/tp_execution/batched.rs:1746-2454).
+//
+// One step = 4 + 9 * layers kernel launches on one HIP stream, optionally
+// replayed from a HIP graph captured once per row count. All per-step inputs
+// (tokens, positions, page tables) live in one device block refreshed by a
+// single host-to-device copy, so a captured graph stays valid across steps.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/ferric_hip.h"
+#include "../../include/ferric_synth.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+constexpr uint32_t kNoLayer = 0xffffffffu;  // QWEN3_NO_LAYER, crates/ferric-spec/src/qwen3.rs:12
+constexpr uint32_t kPageTokens = 16;
+constexpr uint32_t kMaxRows = 32;
+
+thread_local std::string g_create_error;
+
+struct LayerWeights {
+  uint16_t* qkv = nullptr;   // tiled [(qh + 2 kvh) * 128][hidden]
+  uint16_t* o = nullptr;     // tiled [hidden][qh * 128]
+  uint16_t* gu = nullptr;    // tiled, gate/up interleaved by tile [2 * inter][hidden]
+  uint16_t* down = nullptr;  // tiled [hidden][inter]
+  uint16_t* in_norm = nullptr;
+  uint16_t* post_norm = nullptr;
+  uint16_t* q_norm = nullptr;
+  uint16_t* k_norm = nullptr;
+};
+
+struct ProfiledLaunch {
+  uint32_t cls;
+  hipEvent_t begin, end;
+};
+
+}  // namespace
+
+struct fh_ctx {
+  fh_model_desc md{};
+  fh_ctx_options opt{};
+  hipStream_t stream = nullptr;
+  std::vector<void*> device_allocs;
+  std::vector<void*> host_allocs;
+
+  std::vector<LayerWeights> layers;
+  uint16_t* embed = nullptr;  // tiled [vocab][hidden]
+  uint16_t* head = nullptr;   // tiled [vocab][hidden] (== embed when tied)
+  uint16_t* final_norm = nullptr;
+  uint16_t* staging = nullptr;  // row-major upload/synthesis buffer
+  uint64_t staging_elems = 0;
+
+  uint16_t* kv = nullptr;
+  uint64_t kv_slab_elems = 0;  // one K or V cache of one layer: pages * 16 * kvh * 128
+
+  float* cos_t = nullptr;
+  float* sin_t = nullptr;
+
+  uint16_t* hidden = nullptr;
+  uint16_t* xn = nullptr;
+  uint16_t* qkv = nullptr;
+  uint16_t* qrot = nullptr;
+  uint16_t* attn = nullptr;
+  uint16_t* act = nullptr;
+  float* logits = nullptr;
+  float* attn_part = nullptr;
+  void* argmax_scratch = nullptr;
+  uint32_t* choices = nullptr;
+  uint32_t* err = nullptr;
+  uint16_t* capture = nullptr;
+
+  uint32_t* d_meta = nullptr;  // tokens[cap] | positions[cap] | table[cap][stride]
+  uint32_t* h_meta = nullptr;  // pinned mirror
+  uint32_t* h_out = nullptr;   // pinned: choices[cap] | error word
+
+  uint32_t nqkv = 0;
+  std::vector<uint8_t> have;  // which tensors are resident
+  bool poisoned = false;
+  uint64_t last_batch = 0;
+  uint64_t dispatches = 0;
+  uint64_t step_launches = 0;
+  uint32_t last_rows = 0;
+  std::string error;
+
+  std::map<uint32_t, hipGraphExec_t> graphs;
+  std::vector<hipGraph_t> graph_defs;
+  hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+  float last_ms = 0.f;
+
+  bool profiling = false;
+  std::vector<hipEvent_t> prof_events;
+  std::vector<ProfiledLaunch> prof_launches;
+  float class_ms[FH_KC_COUNT] = {};
+  uint32_t class_launches[FH_KC_COUNT] = {};
+
+  // Validation scratch (stamped arrays, sized by physical_pages).
+  std::vector<uint64_t> page_stamp;
+  std::vector<uint64_t> page_seq;
+  std::vector<uint32_t> page_logical;
+  std::vector<uint8_t> page_conflict;
+  std::vector<uint64_t> row_stamp;
+  uint64_t stamp = 0;
+};
+
+namespace {
+
+fh_status fail(fh_ctx* ctx, fh_status st, const std::string& msg) {
+  if (ctx)
+    ctx->error = msg;
+  else
+    g_create_error = msg;
+  return st;
+}
+
+fh_status hip_fail(fh_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, FH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define FH_HIP(ctx, expr)                                  \
+  do {                                                     \
+    hipError_t e_ = (expr);                                \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #expr); \
+  } while (0)
+
+uint32_t tensor_index(uint32_t kind, uint32_t layer, uint32_t layers) {
+  // Globals first (head, embedding, final norm), then 11 per layer.
+  if (kind <= FH_FINAL_NORM) return kind;
+  return 3 + layer * 11 + (kind - FH_INPUT_LAYER_NORM);
+}
+
+bool is_global(uint32_t kind) { return kind <= FH_FINAL_NORM; }
+
+// Rows x columns of each tensor (norms: 1 x width).
+bool tensor_shape(const fh_model_desc& md, uint32_t kind, uint64_t* rows, uint64_t* cols) {
+  const uint64_t h = md.hidden, q = (uint64_t)md.query_heads * 128, kv = (uint64_t)md.kv_heads * 128,
+                 in = md.intermediate, v = md.vocabulary;
+  switch (kind) {
+    case FH_LANGUAGE_MODEL_HEAD: *rows = v; *cols = h; return true;
+    case FH_TOKEN_EMBEDDING: *rows = v; *cols = h; return true;
+    case FH_FINAL_NORM: *rows = 1; *cols = h; return true;
+    case FH_INPUT_LAYER_NORM: *rows = 1; *cols = h; return true;
+    case FH_POST_ATTENTION_LAYER_NORM: *rows = 1; *cols = h; return true;
+    case FH_QUERY_NORM: *rows = 1; *cols = 128; return true;
+    case FH_KEY_NORM: *rows = 1; *cols = 128; return true;
+    case FH_QUERY_PROJECTION: *rows = q; *cols = h; return true;
+    case FH_KEY_PROJECTION: *rows = kv; *cols = h; return true;
+    case FH_VALUE_PROJECTION: *rows = kv; *cols = h; return true;
+    case FH_OUTPUT_PROJECTION: *rows = h; *cols = q; return true;
+    case FH_GATE_PROJECTION: *rows = in; *cols = h; return true;
+    case FH_UP_PROJECTION: *rows = in; *cols = h; return true;
+    case FH_DOWN_PROJECTION: *rows = h; *cols = in; return true;
+    default: return false;
+  }
+}
+
+template <typename T>
+fh_status dalloc(fh_ctx* ctx, T** out, uint64_t count) {
+  void* p = nullptr;
+  uint64_t bytes = std::max<uint64_t>(count * sizeof(T), 256);
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return fail(ctx, FH_ERR_OUT_OF_MEMORY, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  ctx->device_allocs.push_back(p);
+  *out = reinterpret_cast<T*>(p);
+  return FH_OK;
+}
+
+template <typename T>
+fh_status halloc(fh_ctx* ctx, T** out, uint64_t count) {
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, std::max<uint64_t>(count * sizeof(T), 64), hipHostMallocDefault);
+  if (e != hipSuccess) return fail(ctx, FH_ERR_OUT_OF_MEMORY, "hipHostMalloc failed");
+  ctx->host_allocs.push_back(p);
+  *out = reinterpret_cast<T*>(p);
+  return FH_OK;
+}
+
+bool all_weights_present(const fh_ctx* ctx) {
+  for (uint32_t k = 0; k <= FH_FINAL_NORM; ++k) {
+    if (k == FH_LANGUAGE_MODEL_HEAD && ctx->md.tied_embedding) continue;
+    if (!ctx->have[k]) return false;
+  }
+  for (uint32_t l = 0; l < ctx->md.layers; ++l)
+    for (uint32_t k = FH_INPUT_LAYER_NORM; k <= FH_DOWN_PROJECTION; ++k)
+      if (!ctx->have[tensor_index(k, l, ctx->md.layers)]) return false;
+  return true;
+}
+
+uint16_t* kv_cache(fh_ctx* ctx, uint32_t layer, uint32_t which) {
+  return ctx->kv + ((uint64_t)layer * 2 + which) * ctx->kv_slab_elems;
+}
+
+// Places a row-major tensor held in ctx->staging into its resident slot.
+fh_status place_from_staging(fh_ctx* ctx, uint32_t kind, uint32_t layer) {
+  uint64_t rows = 0, cols = 0;
+  tensor_shape(ctx->md, kind, &rows, &cols);
+  hipStream_t s = ctx->stream;
+  const uint32_t q = ctx->md.query_heads * 128, kvc = ctx->md.kv_heads * 128;
+  hipError_t e = hipSuccess;
+  if (is_global(kind)) {
+    if (kind == FH_FINAL_NORM)
+      e = hipMemcpyAsync(ctx->final_norm, ctx->staging, cols * 2, hipMemcpyDeviceToDevice, s);
+    else
+      e = fh::launch_tile_weight(ctx->staging, kind == FH_TOKEN_EMBEDDING ? ctx->embed : ctx->head, (uint32_t)rows,
+                                 (uint32_t)cols, 1, 0, s);
+  } else {
+    LayerWeights& L = ctx->layers[layer];
+    const uint32_t H = ctx->md.hidden;
+    switch (kind) {
+      case FH_INPUT_LAYER_NORM: e = hipMemcpyAsync(L.in_norm, ctx->staging, cols * 2, hipMemcpyDeviceToDevice, s); break;
+      case FH_POST_ATTENTION_LAYER_NORM: e = hipMemcpyAsync(L.post_norm, ctx->staging, cols * 2, hipMemcpyDeviceToDevice, s); break;
+      case FH_QUERY_NORM: e = hipMemcpyAsync(L.q_norm, ctx->staging, cols * 2, hipMemcpyDeviceToDevice, s); break;
+      case FH_KEY_NORM: e = hipMemcpyAsync(L.k_norm, ctx->staging, cols * 2, hipMemcpyDeviceToDevice, s); break;
+      case FH_QUERY_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.qkv, q, H, 1, 0, s); break;
+      case FH_KEY_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.qkv + (uint64_t)q * H, kvc, H, 1, 0, s); break;
+      case FH_VALUE_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.qkv + (uint64_t)(q + kvc) * H, kvc, H, 1, 0, s); break;
+      case FH_OUTPUT_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.o, H, q, 1, 0, s); break;
+      case FH_GATE_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.gu, ctx->md.intermediate, H, 2, 0, s); break;
+      case FH_UP_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.gu, ctx->md.intermediate, H, 2, 1, s); break;
+      case FH_DOWN_PROJECTION: e = fh::launch_tile_weight(ctx->staging, L.down, H, ctx->md.intermediate, 1, 0, s); break;
+      default: return fail(ctx, FH_ERR_INVALID_ARGUMENT, "unknown tensor kind");
+    }
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "placing weight");
+  // The staging buffer is reused by the next upload: finish this one first.
+  FH_HIP(ctx, hipStreamSynchronize(s));
+  ctx->have[tensor_index(kind, layer, ctx->md.layers)] = 1;
+  return FH_OK;
+}
+
+fh_status check_kind_layer(fh_ctx* ctx, uint32_t kind, uint32_t layer) {
+  if (kind > FH_DOWN_PROJECTION) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "tensor kind out of range");
+  if (!is_global(kind) && layer >= ctx->md.layers) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "layer out of range");
+  if (kind == FH_LANGUAGE_MODEL_HEAD && ctx->md.tied_embedding)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "tied model: the LM head is the token embedding");
+  return FH_OK;
+}
+
+// ---- batch validation (batched.rs:1678-1744, 1519-1530) -------------------
+fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                         const uint32_t* output_rows, uint32_t nout) {
+  if (ctx->poisoned)
+    return fail(ctx, FH_ERR_POISONED, "batched execution is closed, poisoned, or missing its v8 head profile");
+  if (!all_weights_present(ctx)) return fail(ctx, FH_ERR_STATE, "model weights are not resident");
+  if (batch_id <= ctx->last_batch || nrows == 0 || nrows > ctx->opt.row_capacity || rows == nullptr)
+    return fail(ctx, FH_ERR_INVALID_BATCH, "foreign, stale, or invalid prepared GPU batch");
+  const uint32_t P = ctx->opt.physical_pages, stride = ctx->opt.page_table_stride;
+  const uint64_t gen = ++ctx->stamp;
+  // Pass 1: page -> (sequence, logical) ownership over every row's list.
+  for (uint32_t i = 0; i < nrows; ++i) {
+    const fh_row& r = rows[i];
+    if (r.page_count > stride || (r.page_count && r.pages == nullptr))
+      return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+    for (uint32_t j = 0; j < r.page_count; ++j) {
+      const uint32_t pg = r.pages[j];
+      if (pg >= P) return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+      if (ctx->page_stamp[pg] != gen) {
+        ctx->page_stamp[pg] = gen;
+        ctx->page_seq[pg] = r.sequence;
+        ctx->page_logical[pg] = j;
+        ctx->page_conflict[pg] = 0;
+      } else if (ctx->page_seq[pg] != r.sequence || ctx->page_logical[pg] != j) {
+        ctx->page_conflict[pg] = 1;
+      }
+    }
+  }
+  // Pass 2: per-row geometry, unique pages, unique write slots.
+  std::vector<uint64_t> slots;
+  slots.reserve(nrows);
+  for (uint32_t i = 0; i < nrows; ++i) {
+    const fh_row& r = rows[i];
+    const uint32_t logical = r.position / kPageTokens;
+    if (r.position >= ctx->opt.context_tokens || r.token >= ctx->md.vocabulary || logical >= r.page_count ||
+        r.pages[logical] != r.writable_page)
+      return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+    const uint64_t row_gen = (gen << 6) | i;
+    for (uint32_t j = 0; j < r.page_count; ++j) {
+      const uint32_t pg = r.pages[j];
+      if (ctx->row_stamp[pg] == row_gen)
+        return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+      ctx->row_stamp[pg] = row_gen;
+    }
+    const uint64_t slot = (uint64_t)r.pages[logical] * kPageTokens + r.position % kPageTokens;
+    if (std::find(slots.begin(), slots.end(), slot) != slots.end())
+      return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+    slots.push_back(slot);
+    const uint32_t wp = r.pages[logical];
+    if (ctx->page_conflict[wp] || ctx->page_seq[wp] != r.sequence || ctx->page_logical[wp] != logical)
+      return fail(ctx, FH_ERR_SHARED_PAGE, "batch writes a page shared with another sequence or logical position");
+  }
+  for (uint32_t i = 0; i < nout; ++i)
+    if (output_rows[i] >= nrows || (i > 0 && output_rows[i] <= output_rows[i - 1]))
+      return fail(ctx, FH_ERR_OUTPUT_ROWS, "output rows must be unique, ascending, and within the batch");
+  return FH_OK;
+}
+
+// ---- the step ---------------------------------------------------------------
+struct Enq {
+  fh_ctx* ctx;
+  uint32_t next_event = 0;
+  uint64_t launches = 0;
+  hipError_t first_error = hipSuccess;
+
+  template <typename F>
+  void run(uint32_t cls, F&& f) {
+    const bool prof = ctx->profiling;
+    hipEvent_t b = nullptr, e = nullptr;
+    if (prof && next_event + 1 < ctx->prof_events.size()) {
+      b = ctx->prof_events[next_event++];
+      e = ctx->prof_events[next_event++];
+      hipEventRecord(b, ctx->stream);
+    }
+    hipError_t err = f();
+    if (err != hipSuccess && first_error == hipSuccess) first_error = err;
+    if (b) {
+      hipEventRecord(e, ctx->stream);
+      ctx->prof_launches.push_back({cls, b, e});
+    }
+  }
+};
+
+hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
+  const fh_model_desc& md = ctx->md;
+  const fh_ctx_options& op = ctx->opt;
+  hipStream_t s = ctx->stream;
+  const uint32_t H = md.hidden, QH = md.query_heads, KVH = md.kv_heads, Q = QH * 128, I = md.intermediate;
+  const uint32_t cap = op.row_capacity, stride = op.page_table_stride, P = op.physical_pages,
+                 C = op.context_tokens;
+  const uint32_t* d_tok = ctx->d_meta;
+  const uint32_t* d_pos = ctx->d_meta + cap;
+  const uint32_t* d_tab = ctx->d_meta + 2 * cap;
+  uint32_t* err = ctx->err;
+  Enq q{ctx};
+  uint64_t n = 0;
+  auto L = [&](uint32_t cls, auto&& f) {
+    q.run(cls, f);
+    ++n;
+  };
+  L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
+  L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, ctx->hidden, R, H, md.vocabulary, err, s); });
+  for (uint32_t l = 0; l < md.layers; ++l) {
+    const LayerWeights& W = ctx->layers[l];
+    uint16_t* kc = kv_cache(ctx, l, 0);
+    uint16_t* vc = kv_cache(ctx, l, 1);
+    L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, W.in_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+    L(FH_KC_QKV_GEMM, [&] {
+      return fh::launch_gemm(ctx->xn, H, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, ctx->qkv, ctx->nqkv, s);
+    });
+    L(FH_KC_QKNORM_ROPE_KV, [&] {
+      return fh::launch_qknorm_rope_kv(ctx->qkv, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, ctx->qrot,
+                                       kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon, err, s);
+    });
+    L(FH_KC_ATTENTION, [&] {
+      return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, R, QH, KVH, stride, P, C,
+                                          err, s);
+    });
+    L(FH_KC_ATTENTION_MERGE, [&] {
+      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, R, QH, C, err, s);
+    });
+    L(FH_KC_O_GEMM, [&] {
+      return fh::launch_gemm(ctx->attn, Q, W.o, R, H, Q, FH_EPI_RESIDUAL, ctx->hidden, ctx->hidden, H, s);
+    });
+    L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, W.post_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+    L(FH_KC_GATE_UP_GEMM, [&] {
+      return fh::launch_gemm(ctx->xn, H, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, ctx->act, I, s);
+    });
+    L(FH_KC_DOWN_GEMM, [&] {
+      return fh::launch_gemm(ctx->act, I, W.down, R, H, I, FH_EPI_RESIDUAL, ctx->hidden, ctx->hidden, H, s);
+    });
+    if (ctx->capture)
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)l * cap * H, (uint64_t)R * H, s);
+      });
+  }
+  L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, ctx->final_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+  L(FH_KC_HEAD_GEMM, [&] {
+    return fh::launch_gemm(ctx->xn, H, ctx->head, R, md.vocabulary, H, FH_EPI_F32, nullptr, ctx->logits,
+                           md.vocabulary, s);
+  });
+  L(FH_KC_ARGMAX, [&] {
+    return fh::launch_argmax(ctx->logits, R, md.vocabulary, ctx->argmax_scratch, ctx->choices, err, s);
+  });
+  ++n;  // argmax is two launches
+  *launches = n;
+  ctx->step_launches = n;
+  return q.first_error;
+}
+
+std::string error_bits(uint32_t e) {
+  std::string s;
+  if (e & fh::ERR_NONFINITE) s += " nonfinite-value";
+  if (e & fh::ERR_TOKEN) s += " token-out-of-vocabulary";
+  if (e & fh::ERR_POSITION) s += " position-out-of-context";
+  if (e & fh::ERR_PAGE) s += " page-out-of-pool";
+  return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fh_last_error(const fh_ctx* ctx) { return ctx ? ctx->error.c_str() : g_create_error.c_str(); }
+
+fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_ctx** out) {
+  if (!md_in || !op_in || !out) return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  const fh_model_desc md = *md_in;
+  const fh_ctx_options op = *op_in;
+  if (md.layers == 0 || md.head_dim != 128 || md.kv_heads == 0 || md.query_heads % md.kv_heads != 0 ||
+      (md.query_heads / md.kv_heads) > 8 || ((md.query_heads / md.kv_heads) & ((md.query_heads / md.kv_heads) - 1)) ||
+      md.hidden % 256 != 0 || md.hidden > 8192 || md.intermediate % 256 != 0 || md.vocabulary % 16 != 0 ||
+      md.vocabulary == 0 || (md.query_heads * 128) % 256 != 0 || md.query_heads + md.kv_heads > 64)
+    return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "unsupported model shape");
+  if (op.row_capacity == 0 || op.row_capacity > kMaxRows || op.physical_pages == 0 || op.context_tokens == 0 ||
+      op.page_table_stride == 0 || op.page_table_stride * kPageTokens < op.context_tokens)
+    return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "unsupported context options");
+
+  fh_ctx* ctx = new fh_ctx();
+  ctx->md = md;
+  ctx->opt = op;
+  auto bail = [&](fh_status st) {
+    g_create_error = ctx->error;
+    fh_destroy(ctx);
+    return st;
+  };
+  hipError_t e = hipSetDevice(op.device);
+  if (e != hipSuccess) return bail(hip_fail(ctx, e, "hipSetDevice"));
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return bail(hip_fail(ctx, e, "hipStreamCreate"));
+  if ((e = hipEventCreate(&ctx->ev_begin)) != hipSuccess || (e = hipEventCreate(&ctx->ev_end)) != hipSuccess)
+    return bail(hip_fail(ctx, e, "hipEventCreate"));
+
+  const uint32_t H = md.hidden, Q = md.query_heads * 128, KV = md.kv_heads * 128, I = md.intermediate,
+                 V = md.vocabulary, cap = op.row_capacity;
+  ctx->nqkv = Q + 2 * KV;
+  ctx->layers.resize(md.layers);
+  ctx->have.assign(3 + 11 * md.layers, 0);
+  fh_status st;
+#define TRY(x)                  \
+  if ((st = (x)) != FH_OK) {    \
+    return bail(st);            \
+  }
+  TRY(dalloc(ctx, &ctx->embed, (uint64_t)V * H));
+  if (md.tied_embedding)
+    ctx->head = ctx->embed;
+  else
+    TRY(dalloc(ctx, &ctx->head, (uint64_t)V * H));
+  TRY(dalloc(ctx, &ctx->final_norm, H));
+  for (auto& L : ctx->layers) {
+    TRY(dalloc(ctx, &L.qkv, (uint64_t)ctx->nqkv * H));
+    TRY(dalloc(ctx, &L.o, (uint64_t)H * Q));
+    TRY(dalloc(ctx, &L.gu, (uint64_t)2 * I * H));
+    TRY(dalloc(ctx, &L.down, (uint64_t)H * I));
+    TRY(dalloc(ctx, &L.in_norm, H));
+    TRY(dalloc(ctx, &L.post_norm, H));
+    TRY(dalloc(ctx, &L.q_norm, 128));
+    TRY(dalloc(ctx, &L.k_norm, 128));
+  }
+  ctx->staging_elems = std::max<uint64_t>({(uint64_t)V * H, (uint64_t)I * H, (uint64_t)Q * H});
+  TRY(dalloc(ctx, &ctx->staging, ctx->staging_elems));
+  ctx->kv_slab_elems = (uint64_t)op.physical_pages * kPageTokens * KV;
+  TRY(dalloc(ctx, &ctx->kv, ctx->kv_slab_elems * 2 * md.layers));
+  TRY(dalloc(ctx, &ctx->cos_t, (uint64_t)op.context_tokens * 64));
+  TRY(dalloc(ctx, &ctx->sin_t, (uint64_t)op.context_tokens * 64));
+  TRY(dalloc(ctx, &ctx->hidden, (uint64_t)cap * H));
+  TRY(dalloc(ctx, &ctx->xn, (uint64_t)cap * H));
+  TRY(dalloc(ctx, &ctx->qkv, (uint64_t)cap * ctx->nqkv));
+  TRY(dalloc(ctx, &ctx->qrot, (uint64_t)cap * Q));
+  TRY(dalloc(ctx, &ctx->attn, (uint64_t)cap * Q));
+  TRY(dalloc(ctx, &ctx->act, (uint64_t)cap * I));
+  TRY(dalloc(ctx, &ctx->logits, (uint64_t)cap * V));
+  TRY(dalloc(ctx, &ctx->attn_part,
+             (uint64_t)cap * md.query_heads * fh::attn_max_splits(op.context_tokens) * fh::kAttnPartialFloats));
+  TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&ctx->argmax_scratch), fh_argmax_scratch_bytes(cap)));
+  TRY(dalloc(ctx, &ctx->choices, cap));
+  TRY(dalloc(ctx, &ctx->err, 64));
+  if (op.capture_hidden) TRY(dalloc(ctx, &ctx->capture, (uint64_t)md.layers * cap * H));
+  const uint64_t meta = 2ull * cap + (uint64_t)cap * op.page_table_stride;
+  TRY(dalloc(ctx, &ctx->d_meta, meta));
+  TRY(halloc(ctx, &ctx->h_meta, meta));
+  TRY(halloc(ctx, &ctx->h_out, cap + 1));
+
+  // RoPE table exactly as rope_bytes (tp_execution.rs:1440-1450): f64
+  // theta^(-pair/64), angle = position * inverse_frequency, cos/sin in f64,
+  // narrowed to f32.
+  {
+    std::vector<float> c((uint64_t)op.context_tokens * 64), sn((uint64_t)op.context_tokens * 64);
+    for (uint32_t p = 0; p < op.context_tokens; ++p)
+      for (uint32_t i = 0; i < 64; ++i) {
+        const double inv = std::pow((double)md.rope_theta, -(double)i / 64.0);
+        const double angle = (double)p * inv;
+        c[(uint64_t)p * 64 + i] = (float)std::cos(angle);
+        sn[(uint64_t)p * 64 + i] = (float)std::sin(angle);
+      }
+    e = hipMemcpy(ctx->cos_t, c.data(), c.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(ctx->sin_t, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return bail(hip_fail(ctx, e, "uploading the RoPE table"));
+  }
+  // Deterministic contents for never-written KV slots and activations.
+  e = fh::launch_fill_u16(ctx->kv, ctx->kv_slab_elems * 2 * md.layers, 0, ctx->stream);
+  if (e == hipSuccess) e = fh::launch_fill_u16(ctx->hidden, (uint64_t)cap * H, 0, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return bail(hip_fail(ctx, e, "initialising the KV pool"));
+
+  ctx->page_stamp.assign(op.physical_pages, 0);
+  ctx->page_seq.assign(op.physical_pages, 0);
+  ctx->page_logical.assign(op.physical_pages, 0);
+  ctx->page_conflict.assign(op.physical_pages, 0);
+  ctx->row_stamp.assign(op.physical_pages, 0);
+#undef TRY
+  *out = ctx;
+  return FH_OK;
+}
+
+void fh_destroy(fh_ctx* ctx) {
+  if (!ctx) return;
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  for (auto& kv : ctx->graphs) hipGraphExecDestroy(kv.second);
+  for (auto g : ctx->graph_defs) hipGraphDestroy(g);
+  for (auto ev : ctx->prof_events) hipEventDestroy(ev);
+  if (ctx->ev_begin) hipEventDestroy(ctx->ev_begin);
+  if (ctx->ev_end) hipEventDestroy(ctx->ev_end);
+  for (void* p : ctx->device_allocs) hipFree(p);
+  for (void* p : ctx->host_allocs) hipHostFree(p);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+fh_status fh_upload_weight(fh_ctx* ctx, uint32_t kind, uint32_t layer, const uint16_t* host, uint64_t elements) {
+  if (!ctx || !host) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null argument");
+  fh_status st = check_kind_layer(ctx, kind, layer);
+  if (st != FH_OK) return st;
+  uint64_t rows = 0, cols = 0;
+  tensor_shape(ctx->md, kind, &rows, &cols);
+  if (elements != rows * cols)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "weight element count does not match the model shape");
+  FH_HIP(ctx, hipMemcpy(ctx->staging, host, elements * 2, hipMemcpyHostToDevice));
+  return place_from_staging(ctx, kind, layer);
+}
+
+fh_status fh_synthesize_weights(fh_ctx* ctx, uint64_t seed, float sigma) {
+  if (!ctx) return FH_ERR_INVALID_ARGUMENT;
+  const float scale = fh_synth_scale(sigma);
+  auto one = [&](uint32_t kind, uint32_t layer) -> fh_status {
+    uint64_t rows = 0, cols = 0;
+    tensor_shape(ctx->md, kind, &rows, &cols);
+    hipError_t e;
+    if (rows == 1)
+      e = fh::launch_fill_u16(ctx->staging, cols, 0x3f80, ctx->stream);  // norms = 1.0
+    else
+      e = fh::launch_synth_fill(ctx->staging, rows * cols, fh_synth_tensor_seed(seed, kind, layer), scale,
+                                ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "synthesising a weight");
+    return place_from_staging(ctx, kind, layer);
+  };
+  fh_status st;
+  for (uint32_t k = 0; k <= FH_FINAL_NORM; ++k) {
+    if (k == FH_LANGUAGE_MODEL_HEAD && ctx->md.tied_embedding) continue;
+    if ((st = one(k, kNoLayer)) != FH_OK) return st;
+  }
+  for (uint32_t l = 0; l < ctx->md.layers; ++l)
+    for (uint32_t k = FH_INPUT_LAYER_NORM; k <= FH_DOWN_PROJECTION; ++k)
+      if ((st = one(k, l)) != FH_OK) return st;
+  return FH_OK;
+}
+
+fh_status fh_download_weight(fh_ctx* ctx, uint32_t kind, uint32_t layer, uint16_t* host, uint64_t elements) {
+  if (!ctx || !host) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null argument");
+  fh_status st = check_kind_layer(ctx, kind, layer);
+  if (st != FH_OK) return st;
+  uint64_t rows = 0, cols = 0;
+  tensor_shape(ctx->md, kind, &rows, &cols);
+  if (elements != rows * cols) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "element count mismatch");
+  if (!ctx->have[tensor_index(kind, layer, ctx->md.layers)]) return fail(ctx, FH_ERR_STATE, "weight not resident");
+  const uint32_t H = ctx->md.hidden, q = ctx->md.query_heads * 128, kvc = ctx->md.kv_heads * 128;
+  const uint16_t* src = nullptr;
+  bool tiled = true;
+  if (is_global(kind)) {
+    if (kind == FH_FINAL_NORM) {
+      src = ctx->final_norm;
+      tiled = false;
+    } else {
+      src = kind == FH_TOKEN_EMBEDDING ? ctx->embed : ctx->head;
+    }
+  } else {
+    const LayerWeights& L = ctx->layers[layer];
+    switch (kind) {
+      case FH_INPUT_LAYER_NORM: src = L.in_norm; tiled = false; break;
+      case FH_POST_ATTENTION_LAYER_NORM: src = L.post_norm; tiled = false; break;
+      case FH_QUERY_NORM: src = L.q_norm; tiled = false; break;
+      case FH_KEY_NORM: src = L.k_norm; tiled = false; break;
+      case FH_QUERY_PROJECTION: src = L.qkv; break;
+      case FH_KEY_PROJECTION: src = L.qkv + (uint64_t)q * H; break;
+      case FH_VALUE_PROJECTION: src = L.qkv + (uint64_t)(q + kvc) * H; break;
+      case FH_OUTPUT_PROJECTION: src = L.o; break;
+      case FH_DOWN_PROJECTION: src = L.down; break;
+      case FH_GATE_PROJECTION:
+      case FH_UP_PROJECTION: {
+        // Gather the even (gate) or odd (up) tiles back into row-major order.
+        const uint32_t I = ctx->md.intermediate, kb = H / 32;
+        std::vector<uint16_t> all((uint64_t)2 * I * H);
+        FH_HIP(ctx, hipMemcpy(all.data(), L.gu, all.size() * 2, hipMemcpyDeviceToHost));
+        const uint32_t parity = kind == FH_UP_PROJECTION ? 1 : 0;
+        for (uint64_t n = 0; n < I; ++n)
+          for (uint32_t k = 0; k < H; ++k) {
+            const uint64_t tile_n = ((n >> 4) * 2 + parity) * 16 + (n & 15);
+            host[n * H + k] = all[fh::tiled_offset((uint32_t)tile_n, k, H)];
+          }
+        (void)kb;
+        return FH_OK;
+      }
+      default: return fail(ctx, FH_ERR_INVALID_ARGUMENT, "unknown tensor kind");
+    }
+  }
+  if (tiled) {
+    hipError_t e = fh::launch_untile_weight(src, ctx->staging, (uint32_t)rows, (uint32_t)cols, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "untile");
+    FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    src = ctx->staging;
+  }
+  FH_HIP(ctx, hipMemcpy(host, src, elements * 2, hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+fh_status fh_kv_fill_synthetic(fh_ctx* ctx, uint64_t seed, float sigma, const fh_row* rows,
+                               const uint64_t* keys, uint32_t nrows, uint32_t context_stride) {
+  if (!ctx || !rows || !keys || nrows == 0) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null argument");
+  const uint32_t stride = ctx->opt.page_table_stride;
+  std::vector<uint32_t> table((uint64_t)nrows * stride, 0xffffffffu), lengths(nrows);
+  uint32_t max_len = 0;
+  for (uint32_t i = 0; i < nrows; ++i) {
+    const fh_row& r = rows[i];
+    const uint32_t need = (r.position + kPageTokens - 1) / kPageTokens;
+    if (r.position > ctx->opt.context_tokens || r.position > context_stride || need > r.page_count ||
+        r.page_count > stride)
+      return fail(ctx, FH_ERR_INVALID_ROW, "KV prefix does not fit the row's pages");
+    for (uint32_t j = 0; j < r.page_count; ++j) {
+      if (r.pages[j] >= ctx->opt.physical_pages) return fail(ctx, FH_ERR_INVALID_ROW, "page outside the pool");
+      table[(uint64_t)i * stride + j] = r.pages[j];
+    }
+    lengths[i] = r.position;
+    max_len = std::max(max_len, r.position);
+  }
+  uint32_t *d_table = nullptr, *d_len = nullptr;
+  uint64_t* d_keys = nullptr;
+  FH_HIP(ctx, hipMalloc(&d_table, table.size() * 4));
+  FH_HIP(ctx, hipMalloc(&d_len, nrows * 4));
+  FH_HIP(ctx, hipMalloc(&d_keys, nrows * 8));
+  hipError_t e = hipMemcpy(d_table, table.data(), table.size() * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(d_len, lengths.data(), nrows * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(d_keys, keys, nrows * 8, hipMemcpyHostToDevice);
+  const float scale = fh_synth_scale(sigma);
+  for (uint32_t l = 0; l < ctx->md.layers && e == hipSuccess && max_len > 0; ++l)
+    for (uint32_t w = 0; w < 2 && e == hipSuccess; ++w)
+      e = fh::launch_kv_fill(kv_cache(ctx, l, w), d_table, d_len, d_keys, nrows, stride, ctx->md.kv_heads,
+                             fh_synth_tensor_seed(seed, FH_SYNTH_KIND_KV_KEY + w, l), scale, context_stride, max_len,
+                             ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(d_table);
+  hipFree(d_len);
+  hipFree(d_keys);
+  if (e != hipSuccess) return hip_fail(ctx, e, "KV fill");
+  return FH_OK;
+}
+
+fh_status fh_read_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page, uint16_t* out,
+                          uint64_t elements) {
+  if (!ctx || !out || layer >= ctx->md.layers || which > 1 || page >= ctx->opt.physical_pages ||
+      elements != (uint64_t)kPageTokens * ctx->md.kv_heads * 128)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad KV page request");
+  FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  FH_HIP(ctx, hipMemcpy(out, kv_cache(ctx, layer, which) + (uint64_t)page * elements, elements * 2,
+                        hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page, const uint16_t* data,
+                           uint64_t elements) {
+  if (!ctx || !data || layer >= ctx->md.layers || which > 1 || page >= ctx->opt.physical_pages ||
+      elements != (uint64_t)kPageTokens * ctx->md.kv_heads * 128)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad KV page request");
+  FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  FH_HIP(ctx, hipMemcpy(kv_cache(ctx, layer, which) + (uint64_t)page * elements, data, elements * 2,
+                        hipMemcpyHostToDevice));
+  return FH_OK;
+}
+
+fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                           const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
+  if (!ctx) return FH_ERR_INVALID_ARGUMENT;
+  if (nout && (!output_rows || !choices_out)) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null output buffers");
+  fh_status st = validate_batch(ctx, batch_id, rows, nrows, output_rows, nout);
+  if (st != FH_OK) return st;
+
+  const uint32_t cap = ctx->opt.row_capacity, stride = ctx->opt.page_table_stride;
+  uint32_t* tok = ctx->h_meta;
+  uint32_t* pos = ctx->h_meta + cap;
+  uint32_t* tab = ctx->h_meta + 2 * cap;
+  for (uint32_t i = 0; i < nrows; ++i) {
+    tok[i] = rows[i].token;
+    pos[i] = rows[i].position;
+    uint32_t* t = tab + (uint64_t)i * stride;
+    std::memcpy(t, rows[i].pages, rows[i].page_count * 4);
+    std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
+  }
+  auto poison = [&](fh_status s2, const std::string& msg) {
+    ctx->poisoned = true;
+    return fail(ctx, s2, msg);
+  };
+  hipStream_t s = ctx->stream;
+  const uint64_t meta_bytes = (2ull * cap + (uint64_t)nrows * stride) * 4;
+  hipError_t e = hipMemcpyAsync(ctx->d_meta, ctx->h_meta, meta_bytes, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("metadata upload: ") + hipGetErrorString(e));
+  hipEventRecord(ctx->ev_begin, s);
+  uint64_t launches = 0;
+  if (ctx->profiling) ctx->prof_launches.clear();
+  if (ctx->opt.use_graphs && !ctx->profiling) {
+    auto it = ctx->graphs.find(nrows);
+    if (it == ctx->graphs.end()) {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+      if (e == hipSuccess) {
+        hipError_t le = enqueue_step(ctx, nrows, &launches);
+        e = hipStreamEndCapture(s, &g);
+        if (e == hipSuccess && le != hipSuccess) e = le;
+      }
+      if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return poison(FH_ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+      }
+      ctx->graph_defs.push_back(g);
+      it = ctx->graphs.emplace(nrows, ge).first;
+    }
+    launches = ctx->step_launches;  // a replay issues what the capture recorded
+    e = hipGraphLaunch(it->second, s);
+  } else {
+    e = enqueue_step(ctx, nrows, &launches);
+  }
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e));
+  hipEventRecord(ctx->ev_end, s);
+  e = hipMemcpyAsync(ctx->h_out, ctx->choices, nrows * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(ctx->h_out + cap, ctx->err, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("step: ") + hipGetErrorString(e));
+  hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);
+  if (ctx->profiling) {
+    for (uint32_t c = 0; c < FH_KC_COUNT; ++c) {
+      ctx->class_ms[c] = 0.f;
+      ctx->class_launches[c] = 0;
+    }
+    for (const auto& pl : ctx->prof_launches) {
+      float ms = 0.f;
+      hipEventElapsedTime(&ms, pl.begin, pl.end);
+      ctx->class_ms[pl.cls] += ms;
+      ctx->class_launches[pl.cls] += 1;
+    }
+  }
+  ctx->last_rows = nrows;
+  const uint32_t errw = ctx->h_out[cap];
+  if (errw != 0) return poison(FH_ERR_NONFINITE, "device rejected the step:" + error_bits(errw));
+  for (uint32_t i = 0; i < nout; ++i) {
+    const uint32_t c = ctx->h_out[output_rows[i]];
+    if (c >= ctx->md.vocabulary) return poison(FH_ERR_NONFINITE, "batched GPU choice outside vocabulary");
+    choices_out[i] = c;
+  }
+  ctx->last_batch = batch_id;
+  ctx->dispatches += launches;
+  return FH_OK;
+}
+
+fh_status fh_read_logits(fh_ctx* ctx, float* out, uint64_t elements) {
+  if (!ctx || !out || elements > (uint64_t)ctx->last_rows * ctx->md.vocabulary)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad logits request");
+  FH_HIP(ctx, hipMemcpy(out, ctx->logits, elements * 4, hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t elements) {
+  if (!ctx || !out || !ctx->capture || layer >= ctx->md.layers ||
+      elements > (uint64_t)ctx->last_rows * ctx->md.hidden)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad hidden-state request (capture_hidden off?)");
+  FH_HIP(ctx, hipMemcpy(out, ctx->capture + (uint64_t)layer * ctx->opt.row_capacity * ctx->md.hidden, elements * 2,
+                        hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+uint32_t fh_row_capacity(const fh_ctx* ctx) { return ctx ? ctx->opt.row_capacity : 0; }
+uint64_t fh_dispatch_count(const fh_ctx* ctx) { return ctx ? ctx->dispatches : 0; }
+float fh_last_step_ms(const fh_ctx* ctx) { return ctx ? ctx->last_ms : 0.f; }
+
+fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled) {
+  if (!ctx) return FH_ERR_INVALID_ARGUMENT;
+  ctx->profiling = enabled != 0;
+  if (ctx->profiling && ctx->prof_events.empty()) {
+    const uint64_t need = 2 * (8 + 12ull * ctx->md.layers);
+    for (uint64_t i = 0; i < need; ++i) {
+      hipEvent_t ev;
+      FH_HIP(ctx, hipEventCreate(&ev));
+      ctx->prof_events.push_back(ev);
+    }
+  }
+  return FH_OK;
+}
+
+fh_status fh_kernel_class_ms(const fh_ctx* ctx, uint32_t cls, float* ms, uint32_t* launches) {
+  if (!ctx || cls >= FH_KC_COUNT || !ms || !launches) return FH_ERR_INVALID_ARGUMENT;
+  *ms = ctx->class_ms[cls];
+  *launches = ctx->class_launches[cls];
+  return FH_OK;
+}
+
+}  // extern "C"

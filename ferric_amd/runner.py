@@ -1,0 +1,215 @@
+"""Host-side mirror of the reference's batch-runner boundary.
+
+`TpBatchRunner` has the method set of the reference's
+`EngineeringTpBatchRunnerV2` (adapters/m1-engineering-execution-v1/src/
+tp_batch_runtime.rs:20-95): `row_capacity`, `execute_batch(batch,
+output_rows) -> BatchOutput{choices}`, `output_head_rows`,
+`expected_dispatch_counts`, `dispatch_counts`, `close`. The prepared-batch
+types mirror `EngineeringTpPreparedRowV1` / `EngineeringTpPreparedBatchV1`
+(tp_paged.rs:257-350). All GPU work and all batch validation happen in
+libferric_hip.so behind the C ABI; this module only marshals.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import FerricError, check, load
+
+PAGE_TOKENS = 16
+
+# Admitted Qwen3 shapes (crates/ferric-spec/src/configuration.rs:107-194).
+QWEN3_8B = dict(layers=36, hidden=4096, query_heads=32, kv_heads=8, head_dim=128, intermediate=12288,
+                vocabulary=151936, tied_embedding=0, rope_theta=1_000_000, rms_epsilon=1e-6)
+QWEN3_0_6B = dict(layers=28, hidden=1024, query_heads=16, kv_heads=8, head_dim=128, intermediate=3072,
+                  vocabulary=151936, tied_embedding=1, rope_theta=1_000_000, rms_epsilon=1e-6)
+
+
+@dataclass(frozen=True)
+class PagedLimits:
+    """Resident envelope (EngineeringTpPagedLimitsV1)."""
+
+    context_tokens: int
+    physical_page_count: int
+    page_table_stride: int
+
+
+@dataclass(frozen=True)
+class PreparedRow:
+    """One sealed row (EngineeringTpPreparedRowV1)."""
+
+    sequence: int
+    token: int
+    position: int
+    physical_pages: tuple
+    writable_physical_page: int
+
+    @property
+    def writable_token_offset(self) -> int:
+        return self.position % PAGE_TOKENS
+
+
+@dataclass
+class PreparedBatch:
+    """Move-only batch metadata (EngineeringTpPreparedBatchV1)."""
+
+    id: int
+    rows: list
+    limits: PagedLimits
+
+
+@dataclass
+class BatchOutput:
+    """EngineeringTpBatchOutputV2: one greedy choice per requested output row."""
+
+    choices: list = field(default_factory=list)
+
+
+def model_desc(cfg: dict) -> _lib.ModelDesc:
+    return _lib.ModelDesc(cfg["layers"], cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["head_dim"],
+                          cfg["intermediate"], cfg["vocabulary"], cfg["tied_embedding"], cfg["rope_theta"],
+                          cfg["rms_epsilon"])
+
+
+def _rows_to_c(rows: Sequence[PreparedRow]):
+    arr = (_lib.Row * len(rows))()
+    keep = []
+    for i, r in enumerate(rows):
+        pages = np.ascontiguousarray(np.asarray(r.physical_pages, dtype=np.uint32))
+        keep.append(pages)
+        arr[i].sequence = r.sequence
+        arr[i].token = r.token
+        arr[i].position = r.position
+        arr[i].pages = pages.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+        arr[i].page_count = len(pages)
+        arr[i].writable_page = r.writable_physical_page
+    return arr, keep
+
+
+class TpBatchRunner:
+    """One-GPU runner behind the reference's batch-runner boundary."""
+
+    def __init__(self, model: dict, limits: PagedLimits, row_capacity: int = 32, use_graphs: bool = True,
+                 capture_hidden: bool = False, device: int = 0):
+        self._lib = load()
+        self.model = dict(model)
+        self.limits = limits
+        self._desc = model_desc(model)
+        self._opts = _lib.CtxOptions(row_capacity, limits.physical_page_count, limits.page_table_stride,
+                                     limits.context_tokens, 1 if use_graphs else 0, 1 if capture_hidden else 0,
+                                     device)
+        ctx = ctypes.c_void_p()
+        st = self._lib.fh_create(ctypes.byref(self._desc), ctypes.byref(self._opts), ctypes.byref(ctx))
+        check(st, None, "fh_create")
+        self._ctx = ctx
+        self._rows_last = 0
+
+    # ---- reference boundary ----
+    def row_capacity(self) -> int:
+        return int(self._lib.fh_row_capacity(self._ctx))
+
+    def execute_batch(self, batch: PreparedBatch, output_rows: Sequence[int]) -> BatchOutput:
+        if batch.limits != self.limits:
+            raise FerricError(2, "foreign, stale, or invalid prepared GPU batch")
+        rows, keep = _rows_to_c(batch.rows)
+        outs = np.ascontiguousarray(np.asarray(output_rows, dtype=np.uint32))
+        choices = np.zeros(max(len(outs), 1), dtype=np.uint32)
+        st = self._lib.fh_execute_batch(self._ctx, batch.id, rows, len(batch.rows),
+                                        outs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(outs),
+                                        choices.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+        del keep
+        check(st, self._ctx)
+        self._rows_last = len(batch.rows)
+        return BatchOutput([int(c) for c in choices[: len(outs)]])
+
+    def output_head_rows(self, physical: int, published: int) -> int:
+        return physical
+
+    def expected_dispatch_counts(self, published: int) -> list:
+        return [6 + 9 * self.model["layers"]]
+
+    def dispatch_counts(self) -> list:
+        return [int(self._lib.fh_dispatch_count(self._ctx))]
+
+    def close(self) -> None:
+        if self._ctx:
+            self._lib.fh_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- setup ----
+    def upload_weight(self, kind: int, layer: int, data: np.ndarray) -> None:
+        data = np.ascontiguousarray(data, dtype=np.uint16).reshape(-1)
+        st = self._lib.fh_upload_weight(self._ctx, kind, layer, data.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                        data.size)
+        check(st, self._ctx)
+
+    def download_weight(self, kind: int, layer: int, elements: int) -> np.ndarray:
+        out = np.zeros(elements, dtype=np.uint16)
+        check(self._lib.fh_download_weight(self._ctx, kind, layer, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                           elements), self._ctx)
+        return out
+
+    def synthesize_weights(self, seed: int, sigma: float = 0.02) -> None:
+        check(self._lib.fh_synthesize_weights(self._ctx, seed, sigma), self._ctx)
+
+    def kv_fill_synthetic(self, seed: int, sigma: float, rows: Sequence[PreparedRow], keys: Sequence[int],
+                          context_stride: int) -> None:
+        crow, keep = _rows_to_c(rows)
+        k = np.ascontiguousarray(np.asarray(keys, dtype=np.uint64))
+        st = self._lib.fh_kv_fill_synthetic(self._ctx, seed, sigma, crow, k.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                                            len(rows), context_stride)
+        del keep
+        check(st, self._ctx)
+
+    # ---- parity readbacks ----
+    def read_logits(self) -> np.ndarray:
+        n = self._rows_last * self.model["vocabulary"]
+        out = np.zeros(n, dtype=np.float32)
+        check(self._lib.fh_read_logits(self._ctx, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n), self._ctx)
+        return out.reshape(self._rows_last, self.model["vocabulary"])
+
+    def read_hidden(self, layer: int) -> np.ndarray:
+        n = self._rows_last * self.model["hidden"]
+        out = np.zeros(n, dtype=np.uint16)
+        check(self._lib.fh_read_hidden(self._ctx, layer, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n),
+              self._ctx)
+        return out.reshape(self._rows_last, self.model["hidden"])
+
+    def read_kv_page(self, layer: int, which: int, page: int) -> np.ndarray:
+        n = PAGE_TOKENS * self.model["kv_heads"] * 128
+        out = np.zeros(n, dtype=np.uint16)
+        check(self._lib.fh_read_kv_page(self._ctx, layer, which, page,
+                                        out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n), self._ctx)
+        return out
+
+    def write_kv_page(self, layer: int, which: int, page: int, data: np.ndarray) -> None:
+        data = np.ascontiguousarray(data, dtype=np.uint16)
+        check(self._lib.fh_write_kv_page(self._ctx, layer, which, page,
+                                         data.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), data.size), self._ctx)
+
+    # ---- timing ----
+    def last_step_ms(self) -> float:
+        return float(self._lib.fh_last_step_ms(self._ctx))
+
+    def set_profiling(self, enabled: bool) -> None:
+        check(self._lib.fh_set_profiling(self._ctx, 1 if enabled else 0), self._ctx)
+
+    def kernel_class_ms(self) -> dict:
+        out = {}
+        for i, name in enumerate(_lib.KERNEL_CLASSES):
+            ms = ctypes.c_float()
+            n = ctypes.c_uint32()
+            check(self._lib.fh_kernel_class_ms(self._ctx, i, ctypes.byref(ms), ctypes.byref(n)), self._ctx)
+            out[name] = (float(ms.value), int(n.value))
+        return out

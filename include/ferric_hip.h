@@ -1,0 +1,269 @@
+/*
+ * ferric_hip.h — C ABI of the MI355X (gfx950) Qwen3 forward-pass hot path.
+ *
+ * This library replaces the GPU work behind Ferric's batch-runner boundary:
+ *
+ *   trait EngineeringTpBatchRunnerV2::execute_batch(&EngineeringTpPreparedBatchV1,
+ *                                                   output_rows) -> choices
+ *   (adapters/m1-engineering-execution-v1/src/tp_batch_runtime.rs:20-95)
+ *
+ * as implemented by EngineeringTpBatchExecutionV2::forward
+ * (adapters/m1-engineering-execution-v1/src/tp_execution/batched.rs:1746-2454).
+ * The caller (scheduler + paged pool, tp_batch_runtime.rs:314-480) keeps page
+ * ownership; this library owns weights and KV device memory, allocated once.
+ *
+ * Conventions: every function returns an fh_status; nothing throws across the
+ * ABI. Host buffers are caller-owned. One HIP stream per context; calls on one
+ * context must come from one thread at a time (the reference's single
+ * controller thread, tp_execution.rs:92-99). bf16 values are uint16_t carriers
+ * (round-to-nearest-even narrowing, NaN quieted with |0x40).
+ *
+ * The fh_op_* entry points run one kernel family on caller-provided device
+ * pointers and a caller-provided stream (hipStream_t passed as void*). They
+ * are the kernel roots of the K1-K7 catalog (crates/ferric-kernels/src/
+ * catalog.rs:47-65) and are what the parity tests drive.
+ */
+#ifndef FERRIC_HIP_H
+#define FERRIC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Errors mirror the reference's TpResult<String> failure classes
+ * (tp_execution.rs:43; batched.rs:1678-1744, 1519-1530). */
+typedef enum fh_status {
+  FH_OK = 0,
+  FH_ERR_INVALID_ARGUMENT = 1, /* bad pointer, shape or descriptor */
+  FH_ERR_INVALID_BATCH = 2,    /* "foreign, stale, or invalid prepared GPU batch" */
+  FH_ERR_INVALID_ROW = 3,      /* "invalid paged row geometry or aliased write slot" */
+  FH_ERR_SHARED_PAGE = 4,      /* "batch writes a page shared with another sequence or logical position" */
+  FH_ERR_OUTPUT_ROWS = 5,      /* "output rows must be unique, ascending, and within the batch" */
+  FH_ERR_NONFINITE = 6,        /* a kernel saw a nonfinite value or an out-of-range index (reference: trap) */
+  FH_ERR_DEVICE = 7,           /* HIP runtime failure */
+  FH_ERR_POISONED = 8,         /* a previous batch failed; only fh_destroy recovers */
+  FH_ERR_OUT_OF_MEMORY = 9,
+  FH_ERR_STATE = 10            /* weights or KV pool not ready */
+} fh_status;
+
+/* Tensor kinds, in the reference's order (crates/ferric-spec/src/qwen3.rs:20-35). */
+typedef enum fh_tensor_kind {
+  FH_LANGUAGE_MODEL_HEAD = 0,
+  FH_TOKEN_EMBEDDING = 1,
+  FH_FINAL_NORM = 2,
+  FH_INPUT_LAYER_NORM = 3,
+  FH_POST_ATTENTION_LAYER_NORM = 4,
+  FH_QUERY_NORM = 5,
+  FH_KEY_NORM = 6,
+  FH_QUERY_PROJECTION = 7,
+  FH_KEY_PROJECTION = 8,
+  FH_VALUE_PROJECTION = 9,
+  FH_OUTPUT_PROJECTION = 10,
+  FH_GATE_PROJECTION = 11,
+  FH_UP_PROJECTION = 12,
+  FH_DOWN_PROJECTION = 13
+} fh_tensor_kind;
+
+/* Model shape; mirrors the admitted Qwen3 configuration
+ * (crates/ferric-spec/src/configuration.rs:107-194). head_dim must be 128,
+ * kv_heads 8, hidden/intermediate multiples of 256. */
+typedef struct fh_model_desc {
+  uint32_t layers;         /* 36 (8B) / 28 (0.6B) */
+  uint32_t hidden;         /* 4096 / 1024 */
+  uint32_t query_heads;    /* 32 / 16 */
+  uint32_t kv_heads;       /* 8 */
+  uint32_t head_dim;       /* 128 */
+  uint32_t intermediate;   /* 12288 / 3072 */
+  uint32_t vocabulary;     /* 151936 */
+  uint32_t tied_embedding; /* 0 (8B) / 1 (0.6B): LM head reads the embedding table */
+  uint32_t rope_theta;     /* 1000000, an integer as in rope_bytes (tp_execution.rs:1440) */
+  float rms_epsilon;       /* 1e-6 */
+} fh_model_desc;
+
+/* Resident-state envelope; mirrors EngineeringTpPagedLimitsV1 (tp_paged.rs:257-350). */
+typedef struct fh_ctx_options {
+  uint32_t row_capacity;      /* rows per batch, 1..32 (reference wide profile: 32) */
+  uint32_t physical_pages;    /* KV pages per layer in the pool */
+  uint32_t page_table_stride; /* page-table entries per row (context_tokens / 16, rounded up) */
+  uint32_t context_tokens;    /* positions must be < context_tokens */
+  uint32_t use_graphs;        /* 1: replay one HIP graph per row count */
+  uint32_t capture_hidden;    /* 1: keep every layer's residual output for fh_read_hidden */
+  int32_t device;             /* HIP device ordinal */
+} fh_ctx_options;
+
+/* One prepared row; mirrors EngineeringTpPreparedRowV1 (tp_paged.rs:257-300). */
+typedef struct fh_row {
+  uint64_t sequence;      /* opaque sequence identity */
+  uint32_t token;         /* input token id (< vocabulary) */
+  uint32_t position;      /* absolute position; the KV slot written is pages[position/16], position%16 */
+  const uint32_t* pages;  /* logical-to-physical page list */
+  uint32_t page_count;    /* <= page_table_stride */
+  uint32_t writable_page; /* must equal pages[position / 16] */
+} fh_row;
+
+typedef struct fh_ctx fh_ctx;
+
+/* ---- context lifecycle (replaces the worker/transport setup of
+ *      EngineeringTpBatchExecutionV2; tp_execution.rs:99-230) ---- */
+
+/* Creates a context: weight storage, KV pool, RoPE table, workspaces. */
+fh_status fh_create(const fh_model_desc* model, const fh_ctx_options* options, fh_ctx** out);
+/* Releases every device allocation (replaces close(), tp_batch_runtime.rs:93). */
+void fh_destroy(fh_ctx* ctx);
+/* Message of the last failure on this context, or of the last failed fh_create when ctx is NULL. */
+const char* fh_last_error(const fh_ctx* ctx);
+
+/* Uploads one row-major bf16 weight [N][K] (nn.Linear layout; norms are [width]).
+ * Replaces the per-rank weight upload (tp_execution.rs:272, UPLOAD_CHUNK_BYTES).
+ * Projections are re-laid out on the device into MFMA tile order. */
+fh_status fh_upload_weight(fh_ctx* ctx, uint32_t kind, uint32_t layer, const uint16_t* host_bf16,
+                           uint64_t elements);
+/* Generates every weight on the device with the ferric_synth.h convention
+ * (projections/embedding ~N(0, sigma), norms = 1.0). */
+fh_status fh_synthesize_weights(fh_ctx* ctx, uint64_t seed, float sigma);
+/* Reads one weight back in row-major order (parity tests). */
+fh_status fh_download_weight(fh_ctx* ctx, uint32_t kind, uint32_t layer, uint16_t* host_bf16,
+                             uint64_t elements);
+
+/* Fills KV positions [0, rows[i].position) of each row's sequence in every layer
+ * with ferric_synth.h samples keyed by (sequence_keys[i], position, head, dim). */
+fh_status fh_kv_fill_synthetic(fh_ctx* ctx, uint64_t seed, float sigma, const fh_row* rows,
+                               const uint64_t* sequence_keys, uint32_t nrows, uint32_t context_stride);
+/* Copies one physical KV page ([16][kv_heads][head_dim] bf16) of one layer. which: 0 = K, 1 = V. */
+fh_status fh_read_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page, uint16_t* out,
+                          uint64_t elements);
+fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page,
+                           const uint16_t* data, uint64_t elements);
+
+/* ---- the hot path ---- */
+
+/* Runs one forward step over the prepared rows and writes the greedy choice of
+ * each requested output row (ascending row indices) to choices_out[nout].
+ * Replaces EngineeringTpBatchRunnerV2::execute_batch (tp_batch_runtime.rs:51-58)
+ * / EngineeringTpBatchExecutionV2::forward (batched.rs:1746-2454). batch_id must
+ * increase strictly (batched.rs:1700). On failure nothing is published and the
+ * context is poisoned (tp_batch_runtime.rs:474). */
+fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                           const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out);
+
+/* Parity readbacks of the last batch: FP32 logits [nrows][vocabulary]; the
+ * residual stream after layer `layer` [nrows][hidden] (needs capture_hidden). */
+fh_status fh_read_logits(fh_ctx* ctx, float* out, uint64_t elements);
+fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t elements);
+
+/* Rows the runner accepts per batch (row_capacity(), tp_batch_runtime.rs:47). */
+uint32_t fh_row_capacity(const fh_ctx* ctx);
+/* Kernel launches issued by successful batches (dispatch_counts(), tp_batch_runtime.rs:89). */
+uint64_t fh_dispatch_count(const fh_ctx* ctx);
+/* Device milliseconds of the last fh_execute_batch, from HIP events on the context stream. */
+float fh_last_step_ms(const fh_ctx* ctx);
+/* Per-kernel-class device time of the last batch when profiling is on (parity/bench aid).
+ * kernel_class indexes fh_kernel_class; returns total ms across launches of that class. */
+fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled);
+fh_status fh_kernel_class_ms(const fh_ctx* ctx, uint32_t kernel_class, float* ms, uint32_t* launches);
+
+typedef enum fh_kernel_class {
+  FH_KC_EMBEDDING = 0,
+  FH_KC_RMSNORM = 1,
+  FH_KC_QKV_GEMM = 2,
+  FH_KC_QKNORM_ROPE_KV = 3,
+  FH_KC_ATTENTION = 4,
+  FH_KC_ATTENTION_MERGE = 5,
+  FH_KC_O_GEMM = 6,
+  FH_KC_GATE_UP_GEMM = 7,
+  FH_KC_DOWN_GEMM = 8,
+  FH_KC_HEAD_GEMM = 9,
+  FH_KC_ARGMAX = 10,
+  FH_KC_COUNT = 11
+} fh_kernel_class;
+
+/* ---- kernel roots on device pointers (K1-K7) ---- */
+
+/* Re-lays a row-major bf16 weight [n][k] into MFMA tile order (n % 16 == 0, k % 32 == 0). */
+fh_status fh_op_tile_weight(const uint16_t* src, uint16_t* dst, uint32_t n, uint32_t k, void* stream);
+/* Interleaves gate [i][k] and up [i][k] into one tiled operand for the fused SwiGLU epilogue. */
+fh_status fh_op_tile_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* dst, uint32_t i,
+                             uint32_t k, void* stream);
+/* Row-major gather back out of tile order (embedding rows; weight readback). */
+fh_status fh_op_untile_weight(const uint16_t* tiled, uint16_t* dst, uint32_t n, uint32_t k, void* stream);
+
+/* K1 embedding: out[r][:] = table[tokens[r]][:] (bit copy); table is tiled [vocab][hidden].
+ * Replaces ferric_qwen3_token_embedding_bf16_copy_v1 (device/qwen3-all-kernels-v1/src/gemm.rs:768). */
+fh_status fh_op_embedding(const uint32_t* tokens, const uint16_t* table_tiled, uint16_t* out,
+                          uint32_t rows, uint32_t hidden, uint32_t vocabulary, uint32_t* error_word,
+                          void* stream);
+
+/* K2 RMSNorm over width 1024/4096 (pure mode) with a wavefront reduction.
+ * Replaces qwen3_rmsnorm_v1 behavior 0 (rmsnorm.rs:380) / wave_rmsnorm_bf16_v15. */
+fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, uint32_t rows,
+                        uint32_t width, float epsilon, uint32_t* error_word, void* stream);
+
+/* K1 projections: out = epilogue(x[m][k] . W[n][k]^T) with FP32 accumulation on MFMA.
+ * epilogue: FH_EPI_BF16 (one RNE), FH_EPI_RESIDUAL (bf16((0 + acc) + residual), may alias out),
+ * FH_EPI_SWIGLU (w from fh_op_tile_gate_up, n = 2*i, out [m][i] = swiglu(bf16(g), bf16(u))),
+ * FH_EPI_F32 (FP32 out, the LM head). m <= 32. Replaces gemm.rs:161/:605 and
+ * device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15/:142/:241, collective.rs:25,
+ * activation.rs:32 and device/qwen3-tp-fp32-head32-kernels-v8/src/projection.rs:66/:186. */
+enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3 };
+fh_status fh_op_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n,
+                     uint32_t k, uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo,
+                     void* stream);
+
+/* K3 per-head QK-norm + split-half RoPE + paged KV append, one launch.
+ * qkv: [rows][(qh + 2*kvh) * 128] projection output; q_out: [rows][qh*128] rotated queries;
+ * k_cache/v_cache: [pages][16][kvh][128]; cos/sin: [context][64] f32 table;
+ * page_table: [rows][stride]. Replaces qwen3_rmsnorm_v1 at width 128 (batched.rs:1956-1982),
+ * qwen3_rope_v1 (rope_kv.rs:102) and qwen3_paged_kv_write_v1 (rope_kv.rs:261). */
+fh_status fh_op_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+                               const float* cos_table, const float* sin_table, const uint32_t* positions,
+                               const uint32_t* page_table, uint16_t* q_out, uint16_t* k_cache,
+                               uint16_t* v_cache, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                               uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
+                               float epsilon, uint32_t* error_word, void* stream);
+
+/* K4 paged GQA decode attention: split-context partials then an ordered merge.
+ * q: [rows][qh*128]; out: [rows][qh*128] bf16; scratch: fh_attention_scratch_bytes().
+ * Replaces qwen3_paged_gqa_decode_bf16_f32_v1 (paged_decode.rs:222) and the split8
+ * partial/merge pair (device/qwen3-tp-c1-split8-attention-kernels-v21/src/attention.rs:16, :214). */
+uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens);
+fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
+                                void* scratch, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                                uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
+                                uint32_t* error_word, void* stream);
+
+/* K6 SwiGLU as its own kernel: out = bf16(silu(g) * u), the stable-sigmoid form of
+ * qwen3_swiglu_bf16_f32_v1 (device/qwen3-all-kernels-v1/src/swiglu.rs:62-120). */
+fh_status fh_op_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t elements,
+                       uint32_t* error_word, void* stream);
+
+/* K7 two-pass lowest-id argmax over FP32 logits [rows][vocabulary]; scratch:
+ * fh_argmax_scratch_bytes(). Replaces device/qwen3-tp-fp32-sharded-argmax-kernels-v13/src/
+ * logits.rs:87/:178 (and the serial v8 logits.rs:30 semantics). */
+uint64_t fh_argmax_scratch_bytes(uint32_t rows);
+fh_status fh_op_argmax(const float* logits, uint32_t rows, uint32_t vocabulary, void* scratch,
+                       uint32_t* choices, uint32_t* error_word, void* stream);
+
+/* Fills dst[0..count) with ferric_synth.h samples of (tensor_seed, index), scale from fh_synth_scale(). */
+fh_status fh_op_synth_fill(uint16_t* dst, uint64_t count, uint64_t tensor_seed, float scale, void* stream);
+
+/* Speculative decoding helpers (integer work), mirrors of
+ * ferric_qwen3_speculative_token_assembly_v1 (logits.rs:587) and
+ * verify_greedy_round (crates/ferric-spec/src/speculation.rs:126). */
+/* target_ids[s][0] = anchors[s]; target_ids[s][1 + i] = draft[i][s] (draft is iteration-major [k][s]). */
+fh_status fh_speculative_token_assembly(const uint32_t* anchors, const uint32_t* draft, uint32_t sequences,
+                                        uint32_t k, uint32_t* target_ids);
+/* accepted = longest prefix with draft[i] == target[i]; emitted = draft[0..accepted] + target[accepted].
+ * Returns FH_ERR_INVALID_ARGUMENT unless target_count == draft_count + 1. */
+fh_status fh_verify_greedy_round(const uint32_t* draft, uint32_t draft_count, const uint32_t* target,
+                                 uint32_t target_count, uint32_t* accepted, uint32_t* emitted,
+                                 uint32_t* emitted_count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRIC_HIP_H */

@@ -1,0 +1,312 @@
+"""Kernel-level parity: each fh_op_* root on the GPU against the CPU oracle.
+
+Bars (stated per test): bit-exact for integer/byte work and wherever the
+GPU keeps the reference's operation order (synthetic fill, tiling, embedding,
+QK-norm + RoPE + KV slot, argmax); within bf16/fp32-accumulate tolerance where
+the GPU reassociates FP32 sums (RMSNorm width 1024/4096, projections,
+attention).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from tests import devutil as du  # noqa: E402
+import ferric_amd  # noqa: E402
+from ferric_amd import _lib  # noqa: E402
+
+LIB = ferric_amd.load()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def rand_bf16(r, n, scale=1.0):
+    return orc.f32_to_bf16(r.standard_normal(n).astype(np.float32) * np.float32(scale))
+
+
+def tile_host(w, n, k):
+    """Numpy statement of the tiled layout: lane = row%16 + 16*((col%32)//8)."""
+    w = w.reshape(n, k)
+    t = w.reshape(n // 16, 16, k // 32, 4, 8)  # nb, r, kb, g, e
+    t = t.transpose(0, 2, 3, 1, 4)  # nb, kb, g, r, e  -> lane = g*16 + r
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def test_synth_fill_matches_oracle_bits():
+    for count, seed in [(1, 3), (4099, 11), (1 << 16, 12345)]:
+        ts = orc.synth_tensor_seed(seed, 7, 2)
+        scale = orc.synth_scale(0.02)
+        d = du.empty(count, np.uint16)
+        _lib.check(LIB.fh_op_synth_fill(du.ptr(d), count, ts, scale, du.stream()))
+        got = du.to_host(d, np.uint16)
+        assert np.array_equal(got, orc.synth(count, ts, scale)), (count, seed)
+
+
+def test_tile_untile_round_trip_and_layout():
+    r = rng(1)
+    for n, k in [(16, 32), (48, 96), (4096, 64)]:
+        w = r.integers(0, 65536, n * k, dtype=np.uint64).astype(np.uint16)
+        dw = du.to_dev(w)
+        dt = du.empty(n * k, np.uint16)
+        _lib.check(LIB.fh_op_tile_weight(du.ptr(dw), du.ptr(dt), n, k, du.stream()))
+        tiled = du.to_host(dt, np.uint16)
+        assert np.array_equal(tiled, tile_host(w, n, k))
+        back = du.empty(n * k, np.uint16)
+        _lib.check(LIB.fh_op_untile_weight(du.ptr(dt), du.ptr(back), n, k, du.stream()))
+        assert np.array_equal(du.to_host(back, np.uint16), w)
+
+
+def test_embedding_bit_copy_from_tiled_table():
+    r = rng(2)
+    vocab, hidden = 160, 256
+    w = r.integers(0, 65536, vocab * hidden, dtype=np.uint64).astype(np.uint16)
+    w[:8] = [0x0000, 0x8000, 0x7F80, 0x7FC1, 0x3F80, 0xBF80, 0x0001, 0x7F7F]  # specials survive a bit copy
+    toks = np.array([0, 159, 17, 17, 64, 3], np.uint32)
+    dw = du.to_dev(w)
+    dt = du.empty(vocab * hidden, np.uint16)
+    _lib.check(LIB.fh_op_tile_weight(du.ptr(dw), du.ptr(dt), vocab, hidden, du.stream()))
+    out = du.empty(len(toks) * hidden, np.uint16)
+    err = du.empty(1, np.uint32)
+    dtok = du.to_dev(toks)
+    _lib.check(LIB.fh_op_embedding(du.ptr(dtok), du.ptr(dt), du.ptr(out), len(toks), hidden, vocab, du.ptr(err),
+                                   du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    assert np.array_equal(du.to_host(out, np.uint16), orc.embedding(toks, w, hidden, vocab))
+    bad = du.to_dev(np.array([5, vocab], np.uint32))  # kept alive by the name
+    _lib.check(LIB.fh_op_embedding(du.ptr(bad), du.ptr(dt), du.ptr(out), 2, hidden, vocab, du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] != 0  # the reference traps on token >= vocab
+
+
+@pytest.mark.parametrize("width", [1024, 4096])
+@pytest.mark.parametrize("rows", [1, 5, 32])
+def test_rmsnorm_within_tolerance(width, rows):
+    r = rng(width + rows)
+    x = rand_bf16(r, rows * width, 3.0)
+    w = rand_bf16(r, width, 1.0)
+    dx, dw_, dy, err = du.to_dev(x), du.to_dev(w), du.empty(rows * width, np.uint16), du.empty(1, np.uint32)
+    _lib.check(LIB.fh_op_rmsnorm(du.ptr(dx), du.ptr(dw_), du.ptr(dy), rows, width, 1e-6, du.ptr(err), du.stream()))
+    got = du.to_host(dy, np.uint16)
+    ref = orc.rmsnorm(x, w, rows, width)
+    assert du.to_host(err, np.uint32)[0] == 0
+    # Reassociated sum of squares: the inverse RMS may differ in its last f32
+    # bits, which can flip the first bf16 rounding (x * inv) by one ulp; the
+    # second rounding (* weight) can carry that to two output ulps.
+    assert du.bf16_ulp_diff(got, ref) <= 2
+    assert du.bf16_rel_err(got, ref) <= 2e-2
+    assert np.mean(got == ref) > 0.99
+
+
+def test_rmsnorm_known_answers():
+    for width in [1024, 4096]:
+        ones = np.full(width, 0x3F80, np.uint16)
+        zeros = np.zeros(2 * width, np.uint16)
+        for x, expect in [(ones, ones), (zeros, zeros)]:
+            rows = len(x) // width
+            dx, dw_, dy, err = du.to_dev(x), du.to_dev(ones), du.empty(len(x), np.uint16), du.empty(1, np.uint32)
+            _lib.check(LIB.fh_op_rmsnorm(du.ptr(dx), du.ptr(dw_), du.ptr(dy), rows, width, 1e-6, du.ptr(err),
+                                         du.stream()))
+            assert np.array_equal(du.to_host(dy, np.uint16), expect)
+        bad = ones.copy()
+        bad[17] = 0x7F80
+        dx, dy, err = du.to_dev(bad), du.empty(width, np.uint16), du.empty(1, np.uint32)
+        dw_ = du.to_dev(ones)
+        _lib.check(LIB.fh_op_rmsnorm(du.ptr(dx), du.ptr(dw_), du.ptr(dy), 1, width, 1e-6, du.ptr(err), du.stream()))
+        assert du.to_host(err, np.uint32)[0] != 0
+
+
+def _gemm_case(m, n, k, epi, seed):
+    r = rng(seed)
+    x = rand_bf16(r, m * k, 1.0)
+    w = rand_bf16(r, n * k, 0.02)
+    dx, dw_ = du.to_dev(x), du.to_dev(w)
+    dt = du.empty(n * k, np.uint16)
+    if epi == _lib.EPI_SWIGLU:
+        i = n // 2
+        gate, up = w[: i * k], w[i * k:]
+        dg, du_ = du.to_dev(gate), du.to_dev(up)
+        _lib.check(LIB.fh_op_tile_gate_up(du.ptr(dg), du.ptr(du_), du.ptr(dt), i, k, du.stream()))
+        out = du.empty(m * i, np.uint16)
+        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), i, du.stream()))
+        got = du.to_host(out, np.uint16)
+        g = orc.gemm(x, gate, m, i, k)
+        u = orc.gemm(x, up, m, i, k)
+        return got, orc.swiglu(g, u)
+    _lib.check(LIB.fh_op_tile_weight(du.ptr(dw_), du.ptr(dt), n, k, du.stream()))
+    if epi == _lib.EPI_F32:
+        out = du.empty(m * n, np.float32)
+        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), n, du.stream()))
+        return du.to_host(out, np.float32), orc.gemm(x, w, m, n, k, f32_out=True)
+    if epi == _lib.EPI_RESIDUAL:
+        res = rand_bf16(r, m * n, 1.0)
+        out = du.to_dev(res)  # in place, as the runtime uses it
+        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, du.ptr(out), du.ptr(out), n, du.stream()))
+        part = orc.gemm(x, w, m, n, k, f32_out=True)
+        return du.to_host(out, np.uint16), orc.residual(part, res)
+    out = du.empty(m * n, np.uint16)
+    _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), n, du.stream()))
+    return du.to_host(out, np.uint16), orc.gemm(x, w, m, n, k)
+
+
+@pytest.mark.parametrize("m", [1, 7, 16, 17, 32])
+@pytest.mark.parametrize("n,k", [(64, 64), (256, 1024), (1024, 4096), (512, 12288)])
+def test_gemm_bf16_and_f32_epilogues(m, n, k):
+    got, ref = _gemm_case(m, n, k, _lib.EPI_F32, m * 7 + n)
+    # FP32 reassociation only: |error| is a few f32 ulps of the partial sums.
+    scale = np.sqrt(k) * 0.02
+    assert np.max(np.abs(got - ref)) <= 2e-5 * scale * 8
+    got, ref = _gemm_case(m, n, k, _lib.EPI_BF16, m * 7 + n + 1)
+    assert du.bf16_close(got, ref, ulps=1)
+    assert np.mean(got == ref) > 0.99
+
+
+@pytest.mark.parametrize("m", [3, 32])
+def test_gemm_residual_and_swiglu_epilogues(m):
+    got, ref = _gemm_case(m, 512, 4096, _lib.EPI_RESIDUAL, 99 + m)
+    assert du.bf16_close(got, ref, ulps=1)
+    assert np.mean(got == ref) > 0.99
+    got, ref = _gemm_case(m, 1024, 1024, _lib.EPI_SWIGLU, 199 + m)
+    assert ref is not None
+    # gate and up are each one bf16 rounding of a reassociated sum (<= 1 ulp),
+    # and SwiGLU multiplies them: <= 2 ulps of the product, plus exp's last ulp.
+    assert du.bf16_close(got, ref, ulps=3)
+    assert np.mean(got == ref) > 0.97
+
+
+def _paged_pool(r, pages, kvh, scale=1.0):
+    n = pages * 16 * kvh * 128
+    return rand_bf16(r, n, scale), rand_bf16(r, n, scale)
+
+
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
+def test_qknorm_rope_kv_bit_exact(qh, kvh):
+    r = rng(qh)
+    rows, pages, stride, context = 9, 64, 64, 1024
+    ld = (qh + 2 * kvh) * 128
+    qkv = rand_bf16(r, rows * ld, 2.0)
+    qn = rand_bf16(r, 128, 1.0)
+    kn = rand_bf16(r, 128, 1.0)
+    positions = np.array([0, 1, 15, 16, 17, 255, 256, 511, 1023], np.uint32)
+    perm = r.permutation(pages).astype(np.uint32)
+    table = np.tile(perm[:stride], (rows, 1)).astype(np.uint32)
+    # distinct slots: each row writes its own position of the shared list
+    cos = np.zeros(context * 64, np.float32)
+    sin = np.zeros(context * 64, np.float32)
+    for p in range(context):
+        c, s = orc.rope_table(p)
+        cos[p * 64:(p + 1) * 64], sin[p * 64:(p + 1) * 64] = c, s
+    kc0, vc0 = _paged_pool(r, pages, kvh)
+    dkc, dvc = du.to_dev(kc0), du.to_dev(vc0)
+    dq = du.empty(rows * qh * 128, np.uint16)
+    err = du.empty(1, np.uint32)
+    keep = [du.to_dev(a) for a in (qkv, qn, kn, cos, sin, positions, table)]
+    _lib.check(LIB.fh_op_qknorm_rope_kv(*[du.ptr(t) for t in keep], du.ptr(dq), du.ptr(dkc), du.ptr(dvc), rows, qh,
+                                        kvh, stride, pages, context, 1e-6, du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    got_q = du.to_host(dq, np.uint16).reshape(rows, qh * 128)
+    got_k = du.to_host(dkc, np.uint16)
+    got_v = du.to_host(dvc, np.uint16)
+    exp_k, exp_v = kc0.copy(), vc0.copy()
+    for i in range(rows):
+        row = qkv[i * ld:(i + 1) * ld]
+        q = orc.rmsnorm(row[: qh * 128], qn, qh, 128)
+        k = orc.rmsnorm(row[qh * 128:(qh + kvh) * 128], kn, kvh, 128)
+        v = row[(qh + kvh) * 128:]
+        c, s = orc.rope_table(int(positions[i]))
+        qr = np.zeros_like(q)
+        kr = np.zeros_like(k)
+        for src, dst, heads in [(q, qr, qh), (k, kr, kvh)]:
+            for h in range(heads):
+                for j in range(64):
+                    a, b = orc.rope_pair(int(src[h * 128 + j]), int(src[h * 128 + j + 64]), float(c[j]), float(s[j]))
+                    dst[h * 128 + j], dst[h * 128 + j + 64] = a, b
+        assert np.array_equal(got_q[i], qr), f"row {i} rotated q"
+        pos = int(positions[i])
+        page = int(table[i, pos // 16])
+        base = orc.cache_index(page, pos % 16, kvh, 0, 0)
+        exp_k[base:base + kvh * 128] = kr
+        exp_v[base:base + kvh * 128] = v
+    assert np.array_equal(got_k, exp_k), "K cache (rotated K at exactly the row slots, nothing else)"
+    assert np.array_equal(got_v, exp_v), "V cache (raw V at exactly the row slots, nothing else)"
+
+
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
+def test_paged_attention_within_tolerance(qh, kvh):
+    r = rng(1000 + qh)
+    pages, stride, context = 600, 520, 8320
+    positions = np.array([0, 15, 16, 255, 256, 257, 1000, 4095, 8319, 77], np.uint32)
+    rows = len(positions)
+    kc, vc = _paged_pool(r, pages, kvh)
+    q = rand_bf16(r, rows * qh * 128, 1.0)
+    table = np.stack([r.permutation(pages)[:stride] for _ in range(rows)]).astype(np.uint32)
+    scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
+    out = du.empty(rows * qh * 128, np.uint16)
+    err = du.empty(1, np.uint32)
+    dkc, dvc = du.to_dev(kc), du.to_dev(vc)
+    dq, dpos, dtab = du.to_dev(q), du.to_dev(positions), du.to_dev(table)
+    _lib.check(LIB.fh_op_paged_attention(du.ptr(dq), du.ptr(dkc), du.ptr(dvc), du.ptr(dpos), du.ptr(dtab),
+                                         du.ptr(out), du.ptr(scratch), rows, qh, kvh, stride, pages, context,
+                                         du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    got = du.to_host(out, np.uint16).reshape(rows, qh, 128)
+    g = qh // kvh
+    worst = 0.0
+    for i in range(rows):
+        for h in range(qh):
+            ref = orc.attention_head(q[(i * qh + h) * 128:(i * qh + h + 1) * 128], kc, vc, table[i], pages,
+                                     int(positions[i]), kvh, h // g)
+            assert ref is not None
+            worst = max(worst, du.bf16_rel_err(got[i, h], ref))
+            if positions[i] == 0:
+                # one key: softmax weight 1, output = V row bits exactly
+                assert np.array_equal(got[i, h], ref)
+    assert worst <= 1e-2, worst
+
+
+def test_swiglu_standalone():
+    r = rng(5)
+    n = 1 << 15
+    gate = rand_bf16(r, n, 4.0)
+    up = rand_bf16(r, n, 1.0)
+    gate[:6] = [0x0000, 0x8000, 0x3F80, 0xBF80, 0x42C8, 0xC2C8]
+    up[:6] = [0x4000, 0x4000, 0x3F80, 0x3F80, 0x3F00, 0x3F00]
+    out = du.empty(n, np.uint16)
+    err = du.empty(1, np.uint32)
+    dg, dup = du.to_dev(gate), du.to_dev(up)
+    _lib.check(LIB.fh_op_swiglu(du.ptr(dg), du.ptr(dup), du.ptr(out), n, du.ptr(err), du.stream()))
+    got = du.to_host(out, np.uint16)
+    ref = orc.swiglu(gate, up)
+    assert du.to_host(err, np.uint32)[0] == 0
+    assert got[0] == 0x0000 and got[1] == 0x8000  # signed zeros (swiglu reference.rs:64-88)
+    assert du.bf16_ulp_diff(got, ref) <= 1  # device exp vs host libm exp: last-ulp differences only
+    assert np.mean(got == ref) > 0.999
+
+
+def test_argmax_lowest_id_ties_and_nonfinite():
+    r = rng(6)
+    rows, vocab = 7, 151936
+    logits = r.standard_normal(rows * vocab).astype(np.float32).reshape(rows, vocab)
+    logits[1, 5] = logits[1, 90000] = 50.0  # exact tie: lowest id wins
+    logits[2, :] = 0.0
+    logits[2, 3] = -0.0  # +0/-0 tie: id 0 wins
+    logits[3, 151935] = 99.0  # last id
+    logits[4, 2374 * 5 - 1] = logits[4, 2374 * 5] = 7.0  # tie across a shard boundary
+    scratch = torch.zeros(LIB.fh_argmax_scratch_bytes(rows) // 4, dtype=torch.int32, device="cuda")
+    ch = du.empty(rows, np.uint32)
+    err = du.empty(1, np.uint32)
+    dl = du.to_dev(logits.reshape(-1))
+    _lib.check(LIB.fh_op_argmax(du.ptr(dl), rows, vocab, du.ptr(scratch), du.ptr(ch), du.ptr(err), du.stream()))
+    got = du.to_host(ch, np.uint32)
+    assert du.to_host(err, np.uint32)[0] == 0
+    for i in range(rows):
+        assert got[i] == orc.argmax_f32(logits[i])[0], i
+    assert got[1] == 5 and got[2] == 0 and got[3] == 151935 and got[4] == 2374 * 5 - 1
+    logits[6, 1234] = np.nan
+    dl = du.to_dev(logits.reshape(-1))
+    _lib.check(LIB.fh_op_argmax(du.ptr(dl), rows, vocab, du.ptr(scratch), du.ptr(ch), du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] != 0
