@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Decode benchmark for the Qwen3 forward-pass hot path on one MI355X.
+
+Default workload (the north-star configuration): Qwen3-8B shape, bf16
+weights ~N(0, 0.02) generated on the device, batch-32 paged decode, per-
+sequence context lengths uniform in [512, 8192] (seeded) of random KV
+(bf16 ~N(0, 1)) in 16-token pages drawn from a shuffled 16384-page pool,
+greedy decode. A step is one fh_execute_batch over the 32 rows: tokens in,
+greedy choices out, KV appended; the chosen tokens feed the next step.
+
+Prints one JSON line (see the contract in the repository's build notes):
+value = whole-job decode tokens/s; roofline = the dominant kernel's
+algorithmic HBM bytes per launch / its average launch time (HIP events on
+the runner's stream, recorded around every launch of the timed steps);
+cpu_baseline = the CPU oracle timed on a bounded sample of the same step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode tokens/s, Qwen3-8B bf16 batch 32 (1 GPU); achieved HBM GB/s % peak"
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (model, batch, (ctx_lo, ctx_hi), physical pages, decode headroom, description)
+    "qwen3-8b-b32": ("8b", 32, (512, 8192), 16384, 128,
+                     "Qwen3-8B shape, batch-32 paged decode, ctx U[512,8192], 16-token pages permuted over a "
+                     "16384-page pool, greedy"),
+    "qwen3-8b-b1": ("8b", 1, (4096, 4096), 300, 128,
+                    "Qwen3-8B shape, batch-1 decode, ctx 4096 of random KV in 16-token pages, greedy"),
+    "qwen3-0.6b-b32": ("0.6b", 32, (128, 2048), 4608, 64,
+                       "Qwen3-0.6B shape, batch-32 paged decode, ctx U[128,2048], shuffled page pool, greedy"),
+}
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=64)
+    p.add_argument("--warmup", type=int, default=4)
+    p.add_argument("--workload", default="qwen3-8b-b32", choices=sorted(WORKLOADS))
+    p.add_argument("--seed", type=int, default=1)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-layers", type=int, default=2, help="layers the CPU oracle sample runs")
+    p.add_argument("--graphs", action="store_true",
+                   help="replay HIP graphs in the timed region (no per-launch events)")
+    return p.parse_args()
+
+
+def kernel_bytes(cfg, rows, positions, stride):
+    """Algorithmic HBM bytes per launch of each kernel class, for one step."""
+    H, QH, KVH, I, V = cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["intermediate"], cfg["vocabulary"]
+    Q, KV = QH * 128, KVH * 128
+    nqkv = Q + 2 * KV
+    kv_read = int(np.sum(np.asarray(positions, np.int64) + 1)) * KV * 2 * 2  # K and V rows, bf16
+    return {
+        "attention": kv_read + rows * Q * 2,
+        "qkv_gemm": nqkv * H * 2 + rows * H * 2 + rows * nqkv * 2,
+        "o_gemm": H * Q * 2 + rows * Q * 2 + rows * H * 2 * 2,
+        "gate_up_gemm": 2 * I * H * 2 + rows * H * 2 + rows * I * 2,
+        "down_gemm": H * I * 2 + rows * I * 2 + rows * H * 2 * 2,
+        "head_gemm": V * H * 2 + rows * H * 2 + rows * V * 4,
+        "rmsnorm": rows * H * 2 * 2 + H * 2,
+        "qknorm_rope_kv": rows * nqkv * 2 + rows * Q * 2 + rows * 2 * KV * 2,
+        "attention_merge": 0,
+        "argmax": rows * V * 4,
+        "embedding": rows * H * 2 * 2,
+    }
+
+
+def step_bytes(cfg, rows, positions):
+    """Algorithmic bytes of one decode step: weights streamed once, embedding
+    rows, KV read over each context (incl. the new token), the new KV rows,
+    FP32 logits."""
+    H, QH, KVH, I, V, L = (cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["intermediate"],
+                           cfg["vocabulary"], cfg["layers"])
+    Q, KV = QH * 128, KVH * 128
+    per_layer = ((Q + 2 * KV) * H + H * Q + 3 * I * H) * 2 + (2 * H + 256) * 2
+    head = V * H * 2  # the LM head, or the tied embedding table it reads
+    weights = L * per_layer + head + H * 2
+    kvb = L * 2 * KV * 2
+    ctx = np.asarray(positions, np.int64) + 1
+    return int(weights + rows * 2 * H + int(np.sum(ctx)) * kvb + rows * kvb + rows * V * 4)
+
+
+def cpu_baseline(cfg, contexts, args, seed):
+    """Times the CPU oracle on one decode step of the same workload restricted
+    to the first args.cpu_layers layers (+ embedding, final norm, FP32 head,
+    argmax), then extrapolates to the full depth."""
+    from oracle import oracle as orc
+
+    sample_cfg = dict(cfg, layers=args.cpu_layers)
+    rows = len(contexts)
+    stride = (max(contexts) + 1 + 15) // 16 + 1
+    pages = sum((c + 1 + 15) // 16 for c in contexts) + rows
+    m = orc.Model(sample_cfg, pages)
+    try:
+        t0 = time.perf_counter()
+        m.synthesize(seed, 0.02)
+        tables = np.full((rows, stride), 0xFFFFFFFF, np.uint32)
+        counts = np.zeros(rows, np.uint32)
+        nxt = 0
+        for i, c in enumerate(contexts):
+            n = (c + 1 + 15) // 16
+            tables[i, :n] = np.arange(nxt, nxt + n, dtype=np.uint32)
+            counts[i] = n
+            nxt += n
+        m.kv_fill(seed, 1.0, tables, stride, contexts, list(range(1, rows + 1)), 1 << 20)
+        setup_s = time.perf_counter() - t0
+        toks = np.random.default_rng(seed).integers(0, cfg["vocabulary"], rows)
+        out = m.forward(toks, contexts, tables, counts, stride, want_logits=False)
+        per_layer = out["seconds_layers"] / args.cpu_layers
+        step_s = per_layer * cfg["layers"] + out["seconds_rest"]
+        return {
+            "value": rows / step_s,
+            "unit": "tokens/s",
+            "cores": orc.threads(),
+            "kind": "port",
+            "sample": (f"1 decode step, batch {rows}, same contexts; first {args.cpu_layers} of {cfg['layers']} layers "
+                       f"({out['seconds_layers']:.2f} s) + embedding/final norm/FP32 head/argmax "
+                       f"({out['seconds_rest']:.2f} s); per-layer time x {cfg['layers']} => {step_s:.2f} s/step "
+                       f"(setup {setup_s:.1f} s untimed)"),
+        }
+    finally:
+        m.close()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every box in this build has one MI355X, so --gpus {args.gpus} is not "
+              f"supported (the batch shards by sequence across GPUs; see the sharding notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ferric_amd
+    from ferric_amd import PagedLimits, PagePool, TpBatchRunner
+
+    name = args.workload
+    model_key, batch, (ctx_lo, ctx_hi), phys_pages, headroom, desc = WORKLOADS[name]
+    cfg = dict(ferric_amd.QWEN3_8B if model_key == "8b" else ferric_amd.QWEN3_0_6B)
+    context_tokens = ctx_hi + headroom + args.warmup + args.steps
+    context_tokens = (context_tokens + 15) // 16 * 16
+    limits = PagedLimits(context_tokens=context_tokens, physical_page_count=phys_pages,
+                         page_table_stride=context_tokens // 16)
+    rng = np.random.default_rng(args.seed)
+    contexts = [int(c) for c in rng.integers(ctx_lo, ctx_hi + 1, batch)]
+
+    t_setup = time.perf_counter()
+    runner = TpBatchRunner(cfg, limits, row_capacity=32, use_graphs=args.graphs)
+    runner.synthesize_weights(args.seed, 0.02)
+    pool = PagePool(limits, seed=args.seed)
+    sids = [pool.admit(c) for c in contexts]
+    fill = [ferric_amd.PreparedRow(s, 0, c, tuple(pool.sequences[s].pages), pool.sequences[s].pages[-1])
+            for s, c in zip(sids, contexts)]
+    runner.kv_fill_synthetic(args.seed, 1.0, fill, sids, context_tokens)
+    tokens = [int(t) for t in rng.integers(0, cfg["vocabulary"], batch)]
+    setup_s = time.perf_counter() - t_setup
+    print(f"# setup {setup_s:.1f} s: {name}, contexts mean {np.mean(contexts):.0f}", file=sys.stderr, flush=True)
+
+    def step(toks):
+        b = pool.prepare(list(zip(sids, toks)))
+        out = runner.execute_batch(b, list(range(batch)))
+        pool.commit(b)
+        return out.choices, [r.position for r in b.rows]
+
+    for _ in range(args.warmup):
+        tokens, _ = step(tokens)
+
+    profile = not args.graphs
+    runner.set_profiling(profile)
+    class_ms = {}
+    class_launches = {}
+    class_bytes = {}
+    step_byte_total = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tokens, positions = step(tokens)
+        if profile:
+            for k, (ms, n) in runner.kernel_class_ms().items():
+                class_ms[k] = class_ms.get(k, 0.0) + ms
+                class_launches[k] = class_launches.get(k, 0) + n
+            for k, b in kernel_bytes(cfg, batch, positions, limits.page_table_stride).items():
+                per_layer = cfg["layers"] if k not in ("head_gemm", "argmax", "embedding") else 1
+                if k == "rmsnorm":
+                    per_layer = 2 * cfg["layers"] + 1
+                class_bytes[k] = class_bytes.get(k, 0) + b * per_layer
+        step_byte_total += step_bytes(cfg, batch, positions)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    runner.set_profiling(False)
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = batch * args.steps / elapsed
+    step_gbs = step_byte_total / elapsed / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (device-generated weights ~N(0,0.02), random KV prefixes ~N(0,1), seeded)",
+        "config": {"workload": desc, "batch": batch, "contexts_mean": round(float(np.mean(contexts)), 1),
+                   "decode_steps_timed": args.steps, "page_tokens": 16, "physical_pages": phys_pages,
+                   "graphs": bool(args.graphs)},
+        "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / PEAK_HBM_GBS, 4),
+                     "bytes_per_step": int(step_byte_total / args.steps)},
+    }
+    if profile and class_ms:
+        dominant = max(class_ms, key=lambda k: class_ms[k])
+        avg_ms = class_ms[dominant] / max(class_launches[dominant], 1)
+        bytes_per_launch = class_bytes.get(dominant, 0) / max(class_launches[dominant], 1)
+        achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+        result["roofline"] = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
+                              "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                              "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 2),
+                              "algorithmic_bytes_per_launch": int(bytes_per_launch)}
+        result["kernels"] = {
+            k: {"ms_per_step": round(class_ms[k] / args.steps, 4),
+                "gbs": round(class_bytes.get(k, 0) / (class_ms[k] * 1e-3) / 1e9, 1) if class_ms[k] > 0 else None}
+            for k in sorted(class_ms, key=lambda k: -class_ms[k])}
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, contexts, args, args.seed)
+    runner.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

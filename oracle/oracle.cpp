@@ -21,6 +21,8 @@
 #include <cstring>
 #include <vector>
 
+#include <omp.h>
+
 #include "../include/ferric_synth.h"
 
 namespace {
@@ -392,11 +394,16 @@ void orc_synth_fill(uint16_t* dst, uint64_t count, uint64_t tensor_seed, float s
   for (int64_t i = 0; i < (int64_t)count; ++i) dst[i] = fh_synth_bf16(tensor_seed, (uint64_t)i, scale);
 }
 
+uint64_t orc_splitmix64(uint64_t x) { return fh_splitmix64(x); }
+
 uint64_t orc_synth_tensor_seed(uint64_t seed, uint32_t kind, uint32_t layer) {
   return fh_synth_tensor_seed(seed, kind, layer);
 }
 
 float orc_synth_scale(double sigma) { return fh_synth_scale(sigma); }
+
+// Threads the OpenMP regions above will use (the CPU baseline's core count).
+int orc_threads(void) { return omp_get_max_threads(); }
 
 }  // extern "C"
 
@@ -523,93 +530,106 @@ void orc_model_kv_fill(OrcModel* m, uint64_t seed, float sigma, const uint32_t* 
     }
 }
 
+// One decoder layer in place on h[rows][hidden], writing K/V to kc/vc.
+// Returns 0, or 1 where the reference would trap.
+static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const uint32_t* positions,
+                     const uint32_t* tables, const uint32_t* page_counts, uint32_t stride, const float* cosr,
+                     const float* sinr, uint16_t* kc, uint16_t* vc) {
+  const uint32_t H = m->hidden, QH = m->qh, KVH = m->kvh, Q = QH * 128, KV = KVH * 128, I = m->inter;
+  std::vector<uint16_t> xn((uint64_t)rows * H), q((uint64_t)rows * Q), k((uint64_t)rows * KV),
+      v((uint64_t)rows * KV), qn((uint64_t)rows * Q), kn((uint64_t)rows * KV), qr((uint64_t)rows * Q),
+      kr((uint64_t)rows * KV), attn((uint64_t)rows * Q), gate((uint64_t)rows * I), up((uint64_t)rows * I),
+      act((uint64_t)rows * I);
+  OrcModel::Layer& W = m->L[l];
+  if (orc_rmsnorm(h, nullptr, W.in_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
+  orc_gemm(xn.data(), W.wq.data(), nullptr, rows, Q, H, 0, q.data(), nullptr);
+  orc_gemm(xn.data(), W.wk.data(), nullptr, rows, KV, H, 0, k.data(), nullptr);
+  orc_gemm(xn.data(), W.wv.data(), nullptr, rows, KV, H, 0, v.data(), nullptr);
+  if (orc_rmsnorm(q.data(), nullptr, W.q_norm.data(), rows * QH, 128, m->eps, 0, nullptr, qn.data())) return 1;
+  if (orc_rmsnorm(k.data(), nullptr, W.k_norm.data(), rows * KVH, 128, m->eps, 0, nullptr, kn.data())) return 1;
+  for (uint32_t r = 0; r < rows; ++r) {
+    for (uint32_t hh = 0; hh < QH; ++hh)
+      for (uint32_t i = 0; i < 64; ++i) {
+        uint16_t o[2];
+        const uint64_t b = (uint64_t)r * Q + hh * 128;
+        orc_rope_pair(qn[b + i], qn[b + i + 64], cosr[r * 64ull + i], sinr[r * 64ull + i], o);
+        qr[b + i] = o[0];
+        qr[b + i + 64] = o[1];
+      }
+    for (uint32_t hh = 0; hh < KVH; ++hh)
+      for (uint32_t i = 0; i < 64; ++i) {
+        uint16_t o[2];
+        const uint64_t b = (uint64_t)r * KV + hh * 128;
+        orc_rope_pair(kn[b + i], kn[b + i + 64], cosr[r * 64ull + i], sinr[r * 64ull + i], o);
+        kr[b + i] = o[0];
+        kr[b + i + 64] = o[1];
+      }
+  }
+  for (uint64_t i = 0; i < (uint64_t)rows * Q; ++i)
+    if (!finite_bf16(qr[i])) return 1;
+  // KV append: every row before any attention (batched.rs:1995-2035).
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint32_t pos = positions[r], lp = pos / 16;
+    if (lp >= page_counts[r]) return 1;
+    const uint32_t page = tables[(uint64_t)r * stride + lp];
+    if (page >= m->pages) return 1;
+    const uint64_t dst = orc_cache_index(page, pos % 16, KVH, 0, 0);
+    std::memcpy(kc + dst, kr.data() + (uint64_t)r * KV, (uint64_t)KV * 2);
+    std::memcpy(vc + dst, v.data() + (uint64_t)r * KV, (uint64_t)KV * 2);
+  }
+  int bad = 0;
+#pragma omp parallel for collapse(2) schedule(dynamic) reduction(| : bad)
+  for (int64_t r = 0; r < (int64_t)rows; ++r)
+    for (int64_t hh = 0; hh < (int64_t)QH; ++hh) {
+      const uint32_t kvhead = (uint32_t)hh / (QH / KVH);
+      bad |= orc_attention_head(qr.data() + (uint64_t)r * Q + hh * 128, kc, vc, tables + (uint64_t)r * stride,
+                                page_counts[r], m->pages, positions[r], KVH, kvhead,
+                                attn.data() + (uint64_t)r * Q + hh * 128);
+    }
+  if (bad) return 1;
+  // O projection: FP32 partial, then the TP1 residual.
+  {
+    std::vector<float> part((uint64_t)rows * H);
+    orc_gemm(attn.data(), W.wo.data(), nullptr, rows, H, Q, 0, nullptr, part.data());
+    orc_residual(part.data(), h, (uint64_t)rows * H, h);
+  }
+  if (orc_rmsnorm(h, nullptr, W.post_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
+  orc_gemm(xn.data(), W.wg.data(), nullptr, rows, I, H, 0, gate.data(), nullptr);
+  orc_gemm(xn.data(), W.wu.data(), nullptr, rows, I, H, 0, up.data(), nullptr);
+  if (orc_swiglu(gate.data(), up.data(), (uint64_t)rows * I, act.data())) return 1;
+  {
+    std::vector<float> part((uint64_t)rows * H);
+    orc_gemm(act.data(), W.wd.data(), nullptr, rows, H, I, 0, nullptr, part.data());
+    orc_residual(part.data(), h, (uint64_t)rows * H, h);
+  }
+  return 0;
+}
+
 // One forward step over `rows` token rows. tables: [rows][stride] page
 // lists (page_counts[r] valid entries). Writes choices[rows]; optional
 // logits [rows][vocab] (FP32), hidden [layers][rows][hidden] (residual stream
 // after each layer) and gaps [rows] (top-2 gap). Returns 0, or 1 + the layer
-// index where the reference would trap (nonfinite / bad index).
+// index where the reference would trap (nonfinite / bad index). seconds (may
+// be NULL) receives the wall time of [all layers, embedding + final norm +
+// head + argmax].
 int orc_model_forward(OrcModel* m, const uint32_t* tokens, const uint32_t* positions, const uint32_t* tables,
                       const uint32_t* page_counts, uint32_t stride, uint32_t rows, uint32_t* choices, float* logits,
-                      uint16_t* hidden_capture, float* gaps) {
-  const uint32_t H = m->hidden, QH = m->qh, KVH = m->kvh, Q = QH * 128, KV = KVH * 128, I = m->inter,
-                 V = m->vocab;
-  std::vector<uint16_t> h((uint64_t)rows * H), xn((uint64_t)rows * H), q((uint64_t)rows * Q),
-      k((uint64_t)rows * KV), v((uint64_t)rows * KV), qn((uint64_t)rows * Q), kn((uint64_t)rows * KV),
-      qr((uint64_t)rows * Q), attn((uint64_t)rows * Q), gate((uint64_t)rows * I), up((uint64_t)rows * I),
-      act((uint64_t)rows * I);
-  const std::vector<uint16_t>& emb = m->embed;
-  if (orc_embedding(tokens, emb.data(), rows, H, V, h.data())) return 1;
+                      uint16_t* hidden_capture, float* gaps, double* seconds) {
+  const uint32_t H = m->hidden, V = m->vocab;
+  const double t_begin = omp_get_wtime();
+  double t_layers_begin = 0.0, t_layers_end = 0.0;
+  std::vector<uint16_t> h((uint64_t)rows * H), xn((uint64_t)rows * H);
+  if (orc_embedding(tokens, m->embed.data(), rows, H, V, h.data())) return 1;
   std::vector<float> cosr((uint64_t)rows * 64), sinr((uint64_t)rows * 64);
   for (uint32_t r = 0; r < rows; ++r) orc_rope_table(positions[r], m->theta, &cosr[r * 64ull], &sinr[r * 64ull]);
+  t_layers_begin = omp_get_wtime();
   for (uint32_t l = 0; l < m->layers; ++l) {
-    OrcModel::Layer& W = m->L[l];
-    const int fail = 1 + (int)l;
-    if (orc_rmsnorm(h.data(), nullptr, W.in_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return fail;
-    orc_gemm(xn.data(), W.wq.data(), nullptr, rows, Q, H, 0, q.data(), nullptr);
-    orc_gemm(xn.data(), W.wk.data(), nullptr, rows, KV, H, 0, k.data(), nullptr);
-    orc_gemm(xn.data(), W.wv.data(), nullptr, rows, KV, H, 0, v.data(), nullptr);
-    if (orc_rmsnorm(q.data(), nullptr, W.q_norm.data(), rows * QH, 128, m->eps, 0, nullptr, qn.data())) return fail;
-    if (orc_rmsnorm(k.data(), nullptr, W.k_norm.data(), rows * KVH, 128, m->eps, 0, nullptr, kn.data())) return fail;
-    std::vector<uint16_t> kr((uint64_t)rows * KV);
-    for (uint32_t r = 0; r < rows; ++r) {
-      for (uint32_t hh = 0; hh < QH; ++hh)
-        for (uint32_t i = 0; i < 64; ++i) {
-          uint16_t o[2];
-          const uint64_t b = (uint64_t)r * Q + hh * 128;
-          orc_rope_pair(qn[b + i], qn[b + i + 64], cosr[r * 64ull + i], sinr[r * 64ull + i], o);
-          qr[b + i] = o[0];
-          qr[b + i + 64] = o[1];
-        }
-      for (uint32_t hh = 0; hh < KVH; ++hh)
-        for (uint32_t i = 0; i < 64; ++i) {
-          uint16_t o[2];
-          const uint64_t b = (uint64_t)r * KV + hh * 128;
-          orc_rope_pair(kn[b + i], kn[b + i + 64], cosr[r * 64ull + i], sinr[r * 64ull + i], o);
-          kr[b + i] = o[0];
-          kr[b + i + 64] = o[1];
-        }
-    }
-    for (uint32_t i = 0; i < (uint64_t)rows * Q; ++i)
-      if (!finite_bf16(qr[i])) return fail;
-    // KV append: every row before any attention (batched.rs:1995-2035).
-    uint16_t* kc = m->cache(l, 0);
-    uint16_t* vc = m->cache(l, 1);
-    for (uint32_t r = 0; r < rows; ++r) {
-      const uint32_t pos = positions[r], lp = pos / 16;
-      if (lp >= page_counts[r]) return fail;
-      const uint32_t page = tables[(uint64_t)r * stride + lp];
-      if (page >= m->pages) return fail;
-      const uint64_t dst = orc_cache_index(page, pos % 16, KVH, 0, 0);
-      std::memcpy(kc + dst, kr.data() + (uint64_t)r * KV, (uint64_t)KV * 2);
-      std::memcpy(vc + dst, v.data() + (uint64_t)r * KV, (uint64_t)KV * 2);
-    }
-    int bad = 0;
-#pragma omp parallel for collapse(2) schedule(dynamic) reduction(| : bad)
-    for (int64_t r = 0; r < (int64_t)rows; ++r)
-      for (int64_t hh = 0; hh < (int64_t)QH; ++hh) {
-        const uint32_t kvhead = (uint32_t)hh / (QH / KVH);
-        bad |= orc_attention_head(qr.data() + (uint64_t)r * Q + hh * 128, kc, vc, tables + (uint64_t)r * stride,
-                                  page_counts[r], m->pages, positions[r], KVH, kvhead,
-                                  attn.data() + (uint64_t)r * Q + hh * 128);
-      }
-    if (bad) return fail;
-    // O projection: FP32 partial, then the TP1 residual.
-    {
-      std::vector<float> part((uint64_t)rows * H);
-      orc_gemm(attn.data(), W.wo.data(), nullptr, rows, H, Q, 0, nullptr, part.data());
-      orc_residual(part.data(), h.data(), (uint64_t)rows * H, h.data());
-    }
-    if (orc_rmsnorm(h.data(), nullptr, W.post_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return fail;
-    orc_gemm(xn.data(), W.wg.data(), nullptr, rows, I, H, 0, gate.data(), nullptr);
-    orc_gemm(xn.data(), W.wu.data(), nullptr, rows, I, H, 0, up.data(), nullptr);
-    if (orc_swiglu(gate.data(), up.data(), (uint64_t)rows * I, act.data())) return fail;
-    {
-      std::vector<float> part((uint64_t)rows * H);
-      orc_gemm(act.data(), W.wd.data(), nullptr, rows, H, I, 0, nullptr, part.data());
-      orc_residual(part.data(), h.data(), (uint64_t)rows * H, h.data());
-    }
+    if (run_layer(m, l, h.data(), rows, positions, tables, page_counts, stride, cosr.data(), sinr.data(),
+                  m->cache(l, 0), m->cache(l, 1)))
+      return 1 + (int)l;
     if (hidden_capture) std::memcpy(hidden_capture + (uint64_t)l * rows * H, h.data(), (uint64_t)rows * H * 2);
   }
+  t_layers_end = omp_get_wtime();
   const int fail = 1 + (int)m->layers;
   if (orc_rmsnorm(h.data(), nullptr, m->final_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return fail;
   std::vector<float> lg((uint64_t)rows * V);
@@ -622,7 +642,30 @@ int orc_model_forward(OrcModel* m, const uint32_t* tokens, const uint32_t* posit
     if (gaps) gaps[r] = gap;
   }
   if (logits) std::memcpy(logits, lg.data(), lg.size() * 4);
+  if (seconds) {
+    const double t_end = omp_get_wtime();
+    seconds[0] = t_layers_end - t_layers_begin;
+    seconds[1] = (t_end - t_begin) - seconds[0];
+  }
   return 0;
+}
+
+
+// Layer `layer` alone, from a caller-given input residual stream hidden_in
+// [rows][hidden] to hidden_out, against a scratch copy of that layer's KV
+// (the model's pool is left untouched). Used to measure one layer's numerical
+// error on the GPU's own input. Returns 0, or 1 where the reference traps.
+int orc_model_layer_isolated(OrcModel* m, uint32_t layer, const uint16_t* hidden_in, const uint32_t* positions,
+                             const uint32_t* tables, const uint32_t* page_counts, uint32_t stride, uint32_t rows,
+                             uint16_t* hidden_out) {
+  const uint64_t n = (uint64_t)rows * m->hidden;
+  std::memcpy(hidden_out, hidden_in, n * 2);
+  std::vector<uint16_t> kc(m->cache(layer, 0), m->cache(layer, 0) + m->slab());
+  std::vector<uint16_t> vc(m->cache(layer, 1), m->cache(layer, 1) + m->slab());
+  std::vector<float> cosr((uint64_t)rows * 64), sinr((uint64_t)rows * 64);
+  for (uint32_t r = 0; r < rows; ++r) orc_rope_table(positions[r], m->theta, &cosr[r * 64ull], &sinr[r * 64ull]);
+  return run_layer(m, layer, hidden_out, rows, positions, tables, page_counts, stride, cosr.data(), sinr.data(),
+                   kc.data(), vc.data());
 }
 
 }  // extern "C"

@@ -75,10 +75,14 @@ def lib():
         L.orc_verify_greedy.argtypes = [_u32p, _c_u32, _u32p, _c_u32, _u32p, _u32p, _u32p]
         L.orc_verify_greedy.restype = ctypes.c_int
         L.orc_synth_fill.argtypes = [_u16p, _c_u64, _c_u64, ctypes.c_float]
+        L.orc_splitmix64.argtypes = [_c_u64]
+        L.orc_splitmix64.restype = _c_u64
         L.orc_synth_tensor_seed.argtypes = [_c_u64, _c_u32, _c_u32]
         L.orc_synth_tensor_seed.restype = _c_u64
         L.orc_synth_scale.argtypes = [ctypes.c_double]
         L.orc_synth_scale.restype = ctypes.c_float
+        L.orc_threads.argtypes = []
+        L.orc_threads.restype = ctypes.c_int
         L.orc_model_create.argtypes = [_c_u32] * 8 + [ctypes.c_float, _c_u32]
         L.orc_model_create.restype = ctypes.c_void_p
         L.orc_model_destroy.argtypes = [ctypes.c_void_p]
@@ -90,8 +94,11 @@ def lib():
         L.orc_model_kv_fill.argtypes = [ctypes.c_void_p, _c_u64, ctypes.c_float, _u32p, _c_u32, _u32p, _u64p, _c_u32,
                                         _c_u32]
         L.orc_model_forward.argtypes = [ctypes.c_void_p, _u32p, _u32p, _u32p, _u32p, _c_u32, _c_u32, _u32p, _f32p,
-                                        _u16p, _f32p]
+                                        _u16p, _f32p, ctypes.POINTER(ctypes.c_double)]
         L.orc_model_forward.restype = ctypes.c_int
+        L.orc_model_layer_isolated.argtypes = [ctypes.c_void_p, _c_u32, _u16p, _u32p, _u32p, _u32p, _c_u32, _c_u32,
+                                               _u16p]
+        L.orc_model_layer_isolated.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -268,6 +275,10 @@ def synth_scale(sigma):
     return float(lib().orc_synth_scale(sigma))
 
 
+def threads() -> int:
+    return int(lib().orc_threads())
+
+
 # ---- whole model ------------------------------------------------------------
 
 class Model:
@@ -307,6 +318,20 @@ class Model:
         lib().orc_model_kv_fill(self.h, seed, sigma, _ptr(tables, _u32p), stride, _ptr(lengths, _u32p),
                                 _ptr(keys, _u64p), len(lengths), context_stride)
 
+    def layer_isolated(self, layer, hidden_in, positions, tables, page_counts, stride):
+        """One layer from a given input residual stream (scratch KV copy)."""
+        hidden_in = np.ascontiguousarray(hidden_in, np.uint16).reshape(-1)
+        positions = np.ascontiguousarray(positions, np.uint32)
+        tables = np.ascontiguousarray(tables, np.uint32)
+        page_counts = np.ascontiguousarray(page_counts, np.uint32)
+        out = np.zeros_like(hidden_in)
+        st = lib().orc_model_layer_isolated(self.h, layer, _ptr(hidden_in, _u16p), _ptr(positions, _u32p),
+                                            _ptr(tables, _u32p), _ptr(page_counts, _u32p), stride, len(positions),
+                                            _ptr(out, _u16p))
+        if st:
+            raise RuntimeError("oracle layer trapped")
+        return out.reshape(len(positions), -1)
+
     def forward(self, tokens, positions, tables, page_counts, stride, want_logits=True, want_hidden=False):
         d = self.desc
         rows = len(tokens)
@@ -318,12 +343,15 @@ class Model:
         gaps = np.zeros(rows, np.float32)
         logits = np.zeros(rows * d["vocabulary"], np.float32) if want_logits else None
         hidden = np.zeros(d["layers"] * rows * d["hidden"], np.uint16) if want_hidden else None
+        seconds = np.zeros(2, np.float64)
         st = lib().orc_model_forward(self.h, _ptr(tokens, _u32p), _ptr(positions, _u32p), _ptr(tables, _u32p),
                                      _ptr(page_counts, _u32p), stride, rows, _ptr(choices, _u32p),
-                                     _ptr(logits, _f32p), _ptr(hidden, _u16p), _ptr(gaps, _f32p))
+                                     _ptr(logits, _f32p), _ptr(hidden, _u16p), _ptr(gaps, _f32p),
+                                     seconds.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
         if st:
             raise RuntimeError(f"oracle forward trapped (code {st})")
-        out = {"choices": choices, "gaps": gaps}
+        out = {"choices": choices, "gaps": gaps, "seconds_layers": float(seconds[0]),
+               "seconds_rest": float(seconds[1])}
         if want_logits:
             out["logits"] = logits.reshape(rows, d["vocabulary"])
         if want_hidden:

@@ -1,0 +1,132 @@
+"""The C ABI boundary on any host: libferric_hip.so loads, exports every
+function include/ferric_hip.h declares with the binding's signature, and its
+host-only entry points (speculative helpers, scratch sizing, argument
+validation) behave like the reference. No GPU calls are made here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import ferric_amd
+from ferric_amd import _lib
+from ferric_amd.pool import PagePool
+from ferric_amd.runner import PagedLimits
+from oracle import oracle as orc
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ferric_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(fh_[a-z_0-9]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ferric_amd.load()
+    names = declared_functions()
+    assert len(names) >= 30
+    bound = {n for n, _, _ in _lib.SIGNATURES}
+    for n in names:
+        assert hasattr(lib, n), f"{n} not exported by libferric_hip.so"
+        assert n in bound, f"{n} has no ctypes signature in ferric_amd/_lib.py"
+    assert bound <= set(names), f"binding names a function the header does not declare: {bound - set(names)}"
+
+
+def test_struct_layouts_match_the_header():
+    # Field counts and widths of the boundary structs.
+    assert ctypes.sizeof(_lib.ModelDesc) == 10 * 4
+    assert ctypes.sizeof(_lib.CtxOptions) == 7 * 4
+    assert _lib.Row.pages.offset == 16 and ctypes.sizeof(_lib.Row) == 32
+
+
+def u32(a):
+    return (ctypes.c_uint32 * len(a))(*a)
+
+
+def test_verify_greedy_round_matches_the_reference_vectors():
+    lib = ferric_amd.load()
+    for draft, target, acc, emitted in [([3, 4, 5], [9, 4, 5, 6], 0, [9]), ([3, 4, 5], [3, 4, 9, 6], 2, [3, 4, 9]),
+                                        ([3, 4, 5], [3, 4, 5, 6], 3, [3, 4, 5, 6])]:
+        a = ctypes.c_uint32()
+        e = (ctypes.c_uint32 * 8)()
+        n = ctypes.c_uint32()
+        st = lib.fh_verify_greedy_round(u32(draft), len(draft), u32(target), len(target), ctypes.byref(a), e,
+                                        ctypes.byref(n))
+        assert st == 0 and a.value == acc and list(e[: n.value]) == emitted
+        assert (acc, emitted) == orc.verify_greedy(draft, target)
+    a, e, n = ctypes.c_uint32(), (ctypes.c_uint32 * 8)(), ctypes.c_uint32()
+    assert lib.fh_verify_greedy_round(u32([3, 4]), 2, u32([3, 4]), 2, ctypes.byref(a), e, ctypes.byref(n)) == 1
+    assert lib.fh_verify_greedy_round(None, 0, None, 0, ctypes.byref(a), e, ctypes.byref(n)) == 1
+
+
+def test_token_assembly_matches_the_oracle():
+    lib = ferric_amd.load()
+    r = np.random.default_rng(0)
+    for s, k in [(1, 4), (8, 4), (32, 4), (3, 0)]:
+        anchors = r.integers(0, 151936, s).tolist()
+        draft = r.integers(0, 151936, s * k).tolist()
+        out = (ctypes.c_uint32 * (s * (k + 1)))()
+        assert lib.fh_speculative_token_assembly(u32(anchors), u32(draft) if k else None, s, k, out) == 0
+        assert list(out) == orc.token_assembly(anchors, draft if k else [0], s, k).tolist()
+
+
+def test_scratch_sizes():
+    lib = ferric_amd.load()
+    # 32 rows x 32 heads x ceil(8320 / 256) partitions x (2 + 128) f32
+    assert lib.fh_attention_scratch_bytes(32, 32, 8320) == 32 * 32 * 33 * 130 * 4
+    assert lib.fh_argmax_scratch_bytes(32) == 32 * 64 * 8
+
+
+def test_ops_reject_bad_shapes_before_any_launch():
+    lib = ferric_amd.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.fh_op_gemm(p, 64, p, 0, 64, 64, 0, None, p, 64, None) == 1  # m = 0
+    assert lib.fh_op_gemm(p, 64, p, 33, 64, 64, 0, None, p, 64, None) == 1  # m > 32
+    assert lib.fh_op_gemm(p, 64, p, 4, 60, 64, 0, None, p, 64, None) == 1  # n % 16
+    assert lib.fh_op_gemm(p, 64, p, 4, 64, 48, 0, None, p, 64, None) == 1  # k % 32
+    assert lib.fh_op_gemm(p, 64, p, 4, 64, 64, 1, None, p, 64, None) == 1  # residual epilogue without residual
+    assert lib.fh_op_gemm(p, 64, p, 4, 64, 64, 9, None, p, 64, None) == 1  # unknown epilogue
+    assert lib.fh_op_tile_weight(p, p, 17, 32, None) == 1
+    assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1
+    assert lib.fh_op_paged_attention(p, p, p, p, p, p, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
+    assert lib.fh_op_paged_attention(p, p, p, p, p, p, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
+
+
+def test_create_rejects_unsupported_shapes_without_touching_the_device():
+    lib = ferric_amd.load()
+    desc = _lib.ModelDesc(2, 1024, 16, 8, 64, 3072, 151936, 1, 1_000_000, 1e-6)  # head_dim 64
+    opts = _lib.CtxOptions(8, 64, 32, 512, 0, 0, 0)
+    ctx = ctypes.c_void_p()
+    assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
+    assert b"unsupported model shape" in lib.fh_last_error(None)
+    desc = _lib.ModelDesc(2, 1024, 16, 8, 128, 3072, 151936, 1, 1_000_000, 1e-6)
+    opts = _lib.CtxOptions(33, 64, 32, 512, 0, 0, 0)  # more rows than the 32-row envelope
+    assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
+    opts = _lib.CtxOptions(8, 64, 16, 512, 0, 0, 0)  # stride * 16 < context
+    assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
+
+
+def test_page_pool_reserves_write_slots_and_consecutive_positions():
+    limits = PagedLimits(context_tokens=128, physical_page_count=20, page_table_stride=8)
+    pool = PagePool(limits, seed=3)
+    a = pool.admit(15)
+    b = pool.admit(0)
+    batch = pool.prepare([(a, 7), (a, 8), (b, 9)])
+    rows = batch.rows
+    assert [r.position for r in rows] == [15, 16, 0]
+    assert rows[0].physical_pages == rows[1].physical_pages and len(rows[0].physical_pages) == 2
+    assert rows[0].writable_physical_page == rows[0].physical_pages[0]
+    assert rows[1].writable_physical_page == rows[1].physical_pages[1]
+    assert rows[1].writable_token_offset == 0
+    pool.commit(batch)
+    assert pool.sequences[a].length == 17 and pool.sequences[b].length == 1
+    all_pages = [p for s in pool.sequences.values() for p in s.pages]
+    assert len(all_pages) == len(set(all_pages))
+    with pytest.raises(ValueError):
+        pool.prepare([(a, 1)] * 120)
