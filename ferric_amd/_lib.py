@@ -43,7 +43,7 @@ GATE_PROJECTION = 11
 UP_PROJECTION = 12
 DOWN_PROJECTION = 13
 
-EPI_BF16, EPI_RESIDUAL, EPI_SWIGLU, EPI_F32 = 0, 1, 2, 3
+EPI_BF16, EPI_RESIDUAL, EPI_SWIGLU, EPI_F32, EPI_PARTIAL = 0, 1, 2, 3, 4
 
 KERNEL_CLASSES = ["embedding", "rmsnorm", "qkv_gemm", "qknorm_rope_kv", "attention", "attention_merge", "o_gemm",
                   "gate_up_gemm", "down_gemm", "head_gemm", "argmax"]
@@ -120,10 +120,14 @@ SIGNATURES = [
     ("fh_op_untile_weight", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_embedding", _st, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     ("fh_op_rmsnorm", _st, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp, _vp]),
-    ("fh_op_gemm", _st, [_vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
-    ("fh_op_qknorm_rope_kv", _st, [_vp] * 10 + [_u32] * 6 + [ctypes.c_float, _vp, _vp]),
+    ("fh_op_gemm", _st, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    ("fh_gemm_default_splits", _u32, [_u32, _u32]),
+    ("fh_op_tile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
+    ("fh_op_untile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
+    ("fh_op_residual_rmsnorm", _st, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32, ctypes.c_float, _vp, _vp]),
+    ("fh_op_qknorm_rope_kv", _st, [_vp, _u32] + [_vp] * 9 + [_u32] * 6 + [ctypes.c_float, _vp, _vp]),
     ("fh_attention_scratch_bytes", _u64, [_u32, _u32, _u32]),
-    ("fh_op_paged_attention", _st, [_vp] * 7 + [_u32] * 6 + [_vp, _vp]),
+    ("fh_op_paged_attention", _st, [_vp] * 6 + [_u32, _vp] + [_u32] * 6 + [_vp, _vp]),
     ("fh_op_swiglu", _st, [_vp, _vp, _vp, _u64, _vp, _vp]),
     ("fh_argmax_scratch_bytes", _u64, [_u32]),
     ("fh_op_argmax", _st, [_vp, _u32, _u32, _vp, _vp, _vp, _vp]),

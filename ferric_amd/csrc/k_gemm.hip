@@ -1,26 +1,31 @@
 // K1 projections for decode (m <= 32 token rows): weight-streaming GEMM on
-// gfx950 MFMA (v_mfma_f32_16x16x32_bf16), FP32 accumulation, fused epilogues.
+// gfx950 MFMA (v_mfma_f32_16x16x32_bf16) with FP32 accumulation.
 //
-// Data layout: the weight W[n][k] is stored in MFMA tile order (common.hpp
-// tiled_offset): each 16x32 tile is one fully coalesced 1 KiB wave load that
-// lands directly in the A-operand registers — no LDS staging, no transpose.
-// The activation x[m][k] (row-major, small, L2-resident) is the B operand:
-// lane l reads 16 contiguous bytes of row (l % 16).
+// Data layout. The weight W[n][k] is stored in MFMA tile order (common.hpp
+// tiled_offset) and the activation x[m][k] in activation tile order
+// (common.hpp act_offset): every operand load of a wave is one contiguous,
+// fully coalesced 1 KiB that lands directly in the MFMA's A or B registers —
+// no LDS staging, no transposes, no partially used cache lines.
 //
-// Work split: a workgroup owns NT consecutive 16-row n-tiles over the whole
-// reduction; its 8 waves split the k-blocks into 8 contiguous ranges, and the
-// 8 partial tiles are added in wave order through LDS (deterministic). The
-// epilogue then writes
-//   FH_EPI_BF16     out = bf16(acc)                      (Q/K/V, gemm.rs:161 beta = 0)
-//   FH_EPI_RESIDUAL out = bf16((0 + acc) + residual)     (O and down + residual,
-//                    v5 collective.rs:25-60; gemm.rs:262-336 beta = 1)
-//   FH_EPI_SWIGLU   out = swiglu(bf16(gate), bf16(up))   (gate/up + K6 fused;
-//                    tiles 2j / 2j+1 are gate / up of the same 16 columns)
-//   FH_EPI_F32      out = acc (f32)                      (FP32 LM head, v8 projection.rs:66)
-// The rounding points are the reference's (one bf16 RNE per projection; gate
-// and up narrowed before SwiGLU); the FP32 summation order is reassociated
-// (k-blocks of 32 per MFMA, 8 wave ranges), as the reference's own wave and
-// MFMA profiles reassociate (v5 projection.rs:15, :241).
+// Work split. A wave owns NT consecutive 16-row n-tiles (NT = 4: 64 weight
+// rows share each activation load, so activation traffic is half the weight
+// traffic at m = 32). Grid = (n / (16 NT), splits): blockIdx.y selects a
+// contiguous range of k-blocks, and the WAVES waves of a workgroup split that
+// range again. Wave partials are added in wave order through LDS
+// (deterministic). Epilogues:
+//   FH_EPI_PARTIAL  FP32 partial sums, one [32][ldo] slab per split; the
+//                    consumer adds the slabs in split order and rounds once
+//                    (residual + RMSNorm, QK-norm) — no atomics, no extra launch
+//   FH_EPI_BF16     out = bf16(acc)                       (gemm.rs:161 beta = 0)
+//   FH_EPI_RESIDUAL out = bf16((0 + acc) + residual)      (v5 collective.rs:25-60)
+//   FH_EPI_SWIGLU   act = swiglu(bf16(gate), bf16(up)), written in activation
+//                    tile order for the down projection; tiles 2j / 2j+1 are
+//                    gate / up of the same 16 columns (K6 fused, swiglu.rs:62-101)
+//   FH_EPI_F32      out = acc                              (FP32 LM head, v8 projection.rs:66)
+// Rounding points are the reference's (one bf16 RNE per projection output;
+// gate and up narrowed before SwiGLU); the FP32 summation order is
+// reassociated (32-wide MFMA k-blocks, wave ranges, splits), as the
+// reference's own wave and MFMA profiles reassociate (v5 projection.rs:15, :241).
 #include "common.hpp"
 #include "kernels.hpp"
 #include "../../include/ferric_hip.h"
@@ -29,37 +34,30 @@ namespace fh {
 
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kGemmThreads = kWaves * 64;
-constexpr int kUnroll = 4;
-
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-template <int NT, int MT, int EPI>
-__global__ __launch_bounds__(kGemmThreads) void gemm_skinny_kernel(const uint16_t* __restrict__ x, uint32_t ldx,
-                                                                   const uint16_t* __restrict__ w, uint32_t m,
-                                                                   uint32_t kb_count,
-                                                                   const uint16_t* residual, void* out,
-                                                                   uint32_t ldo) {
-  __shared__ float red[kWaves][NT * MT * 256];
+template <int NT, int MT, int EPI, int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __restrict__ xt,
+                                                         const uint16_t* __restrict__ w, uint32_t m,
+                                                         uint32_t kb_count, uint32_t kb_split,
+                                                         const uint16_t* residual, void* out, uint32_t ldo) {
+  __shared__ float red[WAVES][NT * MT * 256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t tile0 = blockIdx.x * NT;
-  const uint32_t kb_lo = (kb_count * wave) / kWaves;
-  const uint32_t kb_hi = (kb_count * (wave + 1)) / kWaves;
+  const uint32_t split = blockIdx.y;
+  const uint32_t s_lo = split * kb_split;
+  const uint32_t s_hi = min(s_lo + kb_split, kb_count);
+  const uint32_t s_n = s_hi > s_lo ? s_hi - s_lo : 0;
+  const uint32_t kb_lo = s_lo + (s_n * wave) / WAVES;
+  const uint32_t kb_hi = s_lo + (s_n * (wave + 1)) / WAVES;
 
   const u32x4* wp[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     wp[nt] = reinterpret_cast<const u32x4*>(w) + ((uint64_t)(tile0 + nt) * kb_count + kb_lo) * 64 + lane;
-  const u32x4* xp[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    uint32_t row = mt * 16 + (lane & 15);
-    if (row >= m) row = m - 1;  // rows past m feed columns that are never stored
-    xp[mt] = reinterpret_cast<const u32x4*>(x + (uint64_t)row * ldx + kb_lo * 32 + (lane >> 4) * 8);
-  }
+  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)kb_lo * 128 + lane;
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -68,30 +66,50 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_skinny_kernel(const uint16_
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t steps = kb_hi - kb_lo;
-  uint32_t s = 0;
-  for (; s + kUnroll <= steps; s += kUnroll) {
-    u32x4 wv[kUnroll][NT], xv[kUnroll][MT];
+  // Software pipeline over chunks of UNROLL k-blocks with two register sets:
+  // the next chunk's loads are issued before the current chunk's MFMAs, and
+  // scheduling barriers keep the compiler from sinking them back next to
+  // their uses (which would leave one or two loads in flight per wave).
+  u32x4 wa[UNROLL][NT], xa[UNROLL][MT], wb[UNROLL][NT], xb[UNROLL][MT];
+  auto load = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT], uint32_t s0) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < UNROLL; ++u) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)(s + u) * 64);
+      for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)(s0 + u) * 64);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[mt][(s + u) * 4];
+      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)(s0 + u) * 128 + mt * 64];
     }
+  };
+  auto compute = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT]) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+    for (int u = 0; u < UNROLL; ++u)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(wv[u][nt]), as_b8(xv[u][mt]), acc[nt][mt], 0, 0, 0);
+  };
+  const uint32_t chunks = steps / UNROLL;
+  if (chunks > 0) load(wa, xa, 0);
+  for (uint32_t c = 0; c < chunks; c += 2) {
+    if (c + 1 < chunks) load(wb, xb, (c + 1) * UNROLL);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wa, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < chunks) {
+      if (c + 2 < chunks) load(wa, xa, (c + 2) * UNROLL);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb, xb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  uint32_t s = chunks * UNROLL;
   for (; s < steps; ++s) {
     u32x4 wv[NT], xv[MT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) wv[nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)s * 64);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[mt][s * 4];
+    for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[(uint64_t)s * 128 + mt * 64];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -100,8 +118,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_skinny_kernel(const uint16_
   }
 
   // D layout of the 16x16 MFMA: lane l, element e holds row i = 4*(l/16) + e
-  // (the weight row n) and column j = l % 16 (the activation row m). Store
-  // transposed as [j][i] so the epilogue walks n fastest (coalesced stores).
+  // (weight row n) and column j = l % 16 (activation row m). Stored
+  // transposed as [j][i] so the epilogue walks n fastest.
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -112,39 +130,44 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_skinny_kernel(const uint16_
   __syncthreads();
 
   if constexpr (EPI == FH_EPI_SWIGLU) {
-    static_assert(NT == 2, "SwiGLU epilogue pairs a gate tile with an up tile");
+    static_assert(NT % 2 == 0, "SwiGLU epilogue pairs a gate tile with an up tile");
     bool bad = false;
-    for (int idx = threadIdx.x; idx < MT * 256; idx += kGemmThreads) {
-      const int mt = idx >> 8, j = (idx >> 4) & 15, i = idx & 15;
+    for (int idx = threadIdx.x; idx < (NT / 2) * MT * 256; idx += WAVES * 64) {
+      const int pair = idx / (MT * 256), rem = idx % (MT * 256);
+      const int mt = rem >> 8, j = (rem >> 4) & 15, i = rem & 15;
       const uint32_t row = mt * 16 + j;
-      float g = red[0][(0 * MT + mt) * 256 + j * 16 + i];
-      float u = red[0][(1 * MT + mt) * 256 + j * 16 + i];
+      const int gi = ((2 * pair) * MT + mt) * 256 + j * 16 + i;
+      const int ui = ((2 * pair + 1) * MT + mt) * 256 + j * 16 + i;
+      float g = red[0][gi], u = red[0][ui];
 #pragma unroll
-      for (int wv = 1; wv < kWaves; ++wv) {
-        g += red[wv][(0 * MT + mt) * 256 + j * 16 + i];
-        u += red[wv][(1 * MT + mt) * 256 + j * 16 + i];
+      for (int wv = 1; wv < WAVES; ++wv) {
+        g += red[wv][gi];
+        u += red[wv][ui];
       }
       if (row < m) {
-        uint32_t y = swiglu_bf16(round_bf16(g), round_bf16(u), bad);
-        reinterpret_cast<uint16_t*>(out)[(uint64_t)row * ldo + blockIdx.x * 16 + i] = (uint16_t)y;
+        const uint32_t col = (tile0 / 2 + pair) * 16 + i;
+        const uint32_t y = swiglu_bf16(round_bf16(g), round_bf16(u), bad);
+        reinterpret_cast<uint16_t*>(out)[act_offset(row, col)] = (uint16_t)y;
       }
     }
-    (void)bad;  // nonfinite activations surface at the next norm / the logits
+    (void)bad;  // a nonfinite activation surfaces at the next residual + norm
   } else {
-    for (int idx = threadIdx.x; idx < NT * MT * 256; idx += kGemmThreads) {
+    for (int idx = threadIdx.x; idx < NT * MT * 256; idx += WAVES * 64) {
       const int tm = idx >> 8, j = (idx >> 4) & 15, i = idx & 15;
       const int nt = tm / MT, mt = tm % MT;
       const uint32_t row = mt * 16 + j;
       float v = red[0][idx];
 #pragma unroll
-      for (int wv = 1; wv < kWaves; ++wv) v += red[wv][idx];
+      for (int wv = 1; wv < WAVES; ++wv) v += red[wv][idx];
       if (row >= m) continue;
       const uint64_t n = (uint64_t)(tile0 + nt) * 16 + i;
       const uint64_t o = (uint64_t)row * ldo + n;
-      if constexpr (EPI == FH_EPI_BF16) {
+      if constexpr (EPI == FH_EPI_PARTIAL) {
+        reinterpret_cast<float*>(out)[(uint64_t)split * kMaxRows * ldo + o] = v;
+      } else if constexpr (EPI == FH_EPI_BF16) {
         reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16(v);
       } else if constexpr (EPI == FH_EPI_RESIDUAL) {
-        float r = bf16_to_f32(residual[o]);
+        const float r = bf16_to_f32(residual[o]);
         reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16((0.0f + v) + r);
       } else {
         reinterpret_cast<float*>(out)[o] = v;
@@ -153,35 +176,60 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_skinny_kernel(const uint16_
   }
 }
 
-template <int NT, int EPI>
-hipError_t launch_nt(const uint16_t* x, uint32_t ldx, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k,
-                     const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
-  dim3 grid(n / (16 * NT));
+template <int NT, int EPI, int WAVES, int UNROLL>
+void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
+                    const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+  const uint32_t kb = k / 32;
+  const uint32_t kb_split = (kb + splits - 1) / splits;
+  dim3 grid(n / (16 * NT), splits);
   if (m <= 16)
-    hipLaunchKernelGGL((gemm_skinny_kernel<NT, 1, EPI>), grid, dim3(kGemmThreads), 0, s, x, ldx, w, m, k / 32, residual,
-                       out, ldo);
+    hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
+                       residual, out, ldo);
   else
-    hipLaunchKernelGGL((gemm_skinny_kernel<NT, 2, EPI>), grid, dim3(kGemmThreads), 0, s, x, ldx, w, m, k / 32, residual,
-                       out, ldo);
-  return hipGetLastError();
+    hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
+                       residual, out, ldo);
+}
+
+template <int EPI>
+void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
+                const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+  if (n % 64 == 0)
+    launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  else if constexpr (EPI != FH_EPI_SWIGLU)
+    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  else
+    launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+}
+
+// Splits so that a launch has about 512 workgroups, each split keeping at
+// least 4 k-blocks per wave.
+uint32_t choose_splits(uint32_t n, uint32_t k) {
+  const uint32_t groups = n % 64 == 0 ? n / 64 : n / 16;
+  const uint32_t kb = k / 32;
+  uint32_t s = (512 + groups - 1) / groups;
+  const uint32_t max_s = kb / 16 > 0 ? kb / 16 : 1;
+  if (s > max_s) s = max_s;
+  if (s < 1) s = 1;
+  return s;
 }
 
 }  // namespace
 
-hipError_t launch_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
-                       uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+uint32_t gemm_default_splits(uint32_t n, uint32_t k) { return choose_splits(n, k); }
+
+hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
+                       hipStream_t s) {
+  if (splits == 0) return hipErrorInvalidValue;
   switch (epilogue) {
-    case FH_EPI_BF16:
-      return launch_nt<1, FH_EPI_BF16>(x, ldx, w_tiled, m, n, k, residual, out, ldo, s);
-    case FH_EPI_RESIDUAL:
-      return launch_nt<1, FH_EPI_RESIDUAL>(x, ldx, w_tiled, m, n, k, residual, out, ldo, s);
-    case FH_EPI_SWIGLU:
-      return launch_nt<2, FH_EPI_SWIGLU>(x, ldx, w_tiled, m, n, k, residual, out, ldo, s);
-    case FH_EPI_F32:
-      return launch_nt<1, FH_EPI_F32>(x, ldx, w_tiled, m, n, k, residual, out, ldo, s);
-    default:
-      return hipErrorInvalidValue;
+    case FH_EPI_BF16: launch_epi<FH_EPI_BF16>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
+    case FH_EPI_RESIDUAL: launch_epi<FH_EPI_RESIDUAL>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
+    case FH_EPI_SWIGLU: launch_epi<FH_EPI_SWIGLU>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
+    case FH_EPI_F32: launch_epi<FH_EPI_F32>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
+    case FH_EPI_PARTIAL: launch_epi<FH_EPI_PARTIAL>(x_tiled, w_tiled, m, n, k, splits, residual, out, ldo, s); break;
+    default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
 }  // namespace fh

@@ -107,24 +107,38 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* _
 //  4. rotated k and raw v go to cache[(page*16 + pos%16)][kv_head][128], the
 //     slot of qwen3_paged_kv_write_v1 (rope_kv.rs:261-388).
 __global__ __launch_bounds__(kNormThreads) void qknorm_rope_kv_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const uint32_t* __restrict__ positions,
-    const uint32_t* __restrict__ table, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-    float eps, uint32_t* err) {
+    const uint16_t* __restrict__ qkv, const float* __restrict__ qkv_part, uint32_t splits,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint32_t qh,
+    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err) {
   extern __shared__ float smem[];
-  const uint32_t heads = qh + kvh;
-  float* xs = smem;                  // [heads][129] (padded against bank conflicts)
-  float* inv_s = smem + heads * 129;  // [heads]
+  const uint32_t heads = qh + kvh;            // heads that are normalized and rotated
+  const uint32_t all_heads = qh + 2 * kvh;    // plus the V heads
+  float* xs = smem;                           // [all_heads][129] (padded against bank conflicts)
+  float* inv_s = smem + all_heads * 129;      // [heads]
   const uint32_t row = blockIdx.x;
-  const uint32_t ld = (qh + 2 * kvh) * 128;
-  const uint16_t* src = qkv + (uint64_t)row * ld;
+  const uint32_t ld = all_heads * 128;
 
-  for (uint32_t e = threadIdx.x; e < heads * 64; e += kNormThreads) {
-    uint32_t word = reinterpret_cast<const uint32_t*>(src)[e];
-    uint32_t h = e >> 6, d = (e & 63u) * 2;
-    xs[h * 129 + d] = lo_bf16(word);
-    xs[h * 129 + d + 1] = hi_bf16(word);
+  // Projection outputs of this row, as bf16 values: either the bf16 row, or
+  // bf16(P_0 + P_1 + ...) over the split-K slabs (one rounding, as the
+  // reference's one RNE per projection output).
+  if (splits == 0) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(qkv + (uint64_t)row * ld);
+    for (uint32_t e = threadIdx.x; e < all_heads * 64; e += kNormThreads) {
+      const uint32_t word = src[e];
+      const uint32_t h = e >> 6, d = (e & 63u) * 2;
+      xs[h * 129 + d] = lo_bf16(word);
+      xs[h * 129 + d + 1] = hi_bf16(word);
+    }
+  } else {
+    const uint64_t slab = (uint64_t)kMaxRows * ld;
+    const float* src = qkv_part + (uint64_t)row * ld;
+    for (uint32_t e = threadIdx.x; e < all_heads * 128; e += kNormThreads) {
+      float acc = src[e];
+      for (uint32_t sp = 1; sp < splits; ++sp) acc += src[sp * slab + e];
+      xs[(e >> 7) * 129 + (e & 127u)] = round_bf16(acc);
+    }
   }
   __syncthreads();
   if (threadIdx.x < heads) {
@@ -179,11 +193,110 @@ __global__ __launch_bounds__(kNormThreads) void qknorm_rope_kv_kernel(
     }
   }
   if (slot_ok) {
-    const uint32_t* vsrc = reinterpret_cast<const uint32_t*>(src + (qh + kvh) * 128);
+    // Raw V (neither normalized nor rotated) into the same slot.
     uint32_t* vdst = reinterpret_cast<uint32_t*>(v_cache + (uint64_t)slot_base * 128);
-    for (uint32_t e = threadIdx.x; e < kvh * 64; e += kNormThreads) vdst[e] = vsrc[e];
+    for (uint32_t e = threadIdx.x; e < kvh * 64; e += kNormThreads) {
+      const float* xv = xs + (heads + (e >> 6)) * 129 + (e & 63u) * 2;
+      vdst[e] = f32_to_bf16(xv[0]) | (f32_to_bf16(xv[1]) << 16);
+    }
   }
   if (bad) raise_error(err, ERR_NONFINITE);
+}
+
+// Residual + RMSNorm (see fh_op_residual_rmsnorm): one workgroup per row,
+// 16-byte chunks c = tid, tid + 256, ... of the row.
+__global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t* __restrict__ hidden,
+                                                                        const float* __restrict__ part,
+                                                                        uint32_t splits,
+                                                                        const uint16_t* __restrict__ w,
+                                                                        uint16_t* __restrict__ y, uint32_t y_tiled,
+                                                                        uint32_t width, float eps, uint32_t* err) {
+  __shared__ float red[kNormThreads / 64];
+  const uint32_t row = blockIdx.x;
+  uint16_t* hr = hidden + (uint64_t)row * width;
+  const uint32_t chunks = width / 8;
+  constexpr int kMaxPerThread = 4;  // width <= 8192
+  const uint64_t slab = (uint64_t)kMaxRows * width;
+  uint4 v[kMaxPerThread];
+  float sum = 0.f;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < kMaxPerThread; ++j) {
+    const uint32_t c = threadIdx.x + j * kNormThreads;
+    if (c < chunks) {
+      v[j] = *reinterpret_cast<const uint4*>(hr + c * 8);
+      if (splits) {
+        // h = bf16((0 + (P_0 + P_1 + ...)) + h), v5 collective.rs:25-60 with
+        // the split-K slabs added in split order.
+        const float* pr = part + (uint64_t)row * width + c * 8;
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = pr[e];
+        for (uint32_t sp = 1; sp < splits; ++sp)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] += pr[sp * slab + e];
+        uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = f32_to_bf16((0.0f + a[2 * q]) + lo_bf16(words[q]));
+          const uint32_t hi = f32_to_bf16((0.0f + a[2 * q + 1]) + hi_bf16(words[q]));
+          words[q] = lo | (hi << 16);
+        }
+        v[j] = make_uint4(words[0], words[1], words[2], words[3]);
+        *reinterpret_cast<uint4*>(hr + c * 8) = v[j];
+      }
+      const uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = lo_bf16(words[q]), b = hi_bf16(words[q]);
+        bad |= !is_finite_f32(a) | !is_finite_f32(b);
+        sum = sum + a * a;
+        sum = sum + b * b;
+      }
+    }
+  }
+  const float total = block_sum_ordered(sum, red);
+  const float inv = inverse_rms(total, (float)width, eps);
+  if (!is_finite_f32(total) || !is_finite_f32(inv)) bad = true;
+#pragma unroll
+  for (int j = 0; j < kMaxPerThread; ++j) {
+    const uint32_t c = threadIdx.x + j * kNormThreads;
+    if (c < chunks) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c * 8);
+      const uint32_t xs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a = norm_weight_bf16(lo_bf16(xs[q]), inv, lo_bf16(ws[q]));
+        const uint32_t b = norm_weight_bf16(hi_bf16(xs[q]), inv, hi_bf16(ws[q]));
+        bad |= ((a & 0x7f80u) == 0x7f80u) | ((b & 0x7f80u) == 0x7f80u);
+        o[q] = a | (b << 16);
+      }
+      const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
+      if (y_tiled)
+        *reinterpret_cast<uint4*>(y + act_offset(row, c * 8)) = ov;
+      else
+        *reinterpret_cast<uint4*>(y + (uint64_t)row * width + c * 8) = ov;
+    }
+  }
+  if (bad) raise_error(err, ERR_NONFINITE);
+}
+
+// Row-major <-> activation tile order, one 16-byte chunk per thread.
+__global__ __launch_bounds__(kNormThreads) void tile_activation_kernel(const uint16_t* __restrict__ x,
+                                                                       uint16_t* __restrict__ xt, uint32_t m,
+                                                                       uint32_t k, uint32_t to_tiled) {
+  const uint32_t chunks = m * (k / 8);
+  for (uint32_t c = blockIdx.x * kNormThreads + threadIdx.x; c < chunks; c += gridDim.x * kNormThreads) {
+    const uint32_t row = c / (k / 8), col = (c % (k / 8)) * 8;
+    if (to_tiled)
+      *reinterpret_cast<uint4*>(xt + act_offset(row, col)) =
+          *reinterpret_cast<const uint4*>(x + (uint64_t)row * k + col);
+    else
+      *reinterpret_cast<uint4*>(const_cast<uint16_t*>(x) + (uint64_t)row * k + col) =
+          *reinterpret_cast<const uint4*>(xt + act_offset(row, col));
+  }
 }
 
 __global__ __launch_bounds__(kNormThreads) void swiglu_kernel(const uint16_t* __restrict__ gate,
@@ -203,14 +316,33 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, uin
   return hipGetLastError();
 }
 
-hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
-                                 const float* cos_t, const float* sin_t, const uint32_t* positions,
-                                 const uint32_t* table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
-                                 uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
-                                 uint32_t context, float eps, uint32_t* err, hipStream_t s) {
-  size_t lds = ((size_t)(qh + kvh) * 129 + (qh + kvh)) * sizeof(float);
-  hipLaunchKernelGGL(qknorm_rope_kv_kernel, dim3(rows), dim3(kNormThreads), lds, s, qkv, q_norm, k_norm, cos_t, sin_t,
-                     positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context, eps, err);
+hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uint32_t splits, const uint16_t* q_norm,
+                                 const uint16_t* k_norm, const float* cos_t, const float* sin_t,
+                                 const uint32_t* positions, const uint32_t* table, uint16_t* q_out,
+                                 uint16_t* k_cache, uint16_t* v_cache, uint32_t rows, uint32_t qh, uint32_t kvh,
+                                 uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err,
+                                 hipStream_t s) {
+  size_t lds = ((size_t)(qh + 2 * kvh) * 129 + (qh + kvh)) * sizeof(float);
+  hipLaunchKernelGGL(qknorm_rope_kv_kernel, dim3(rows), dim3(kNormThreads), lds, s, qkv, qkv_part, splits, q_norm,
+                     k_norm, cos_t, sin_t, positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context,
+                     eps, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* w,
+                                   uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float eps,
+                                   uint32_t* err, hipStream_t s) {
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, y,
+                     y_tiled, width, eps, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, uint32_t to_tiled,
+                                  hipStream_t s) {
+  const uint32_t chunks = m * (k / 8);
+  const uint32_t grid = (chunks + kNormThreads - 1) / kNormThreads;
+  hipLaunchKernelGGL(tile_activation_kernel, dim3(grid ? grid : 1), dim3(kNormThreads), 0, s, x, x_tiled, m, k,
+                     to_tiled);
   return hipGetLastError();
 }
 

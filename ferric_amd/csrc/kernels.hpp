@@ -7,13 +7,17 @@
 
 namespace fh {
 
-// Attention split size: each partial workgroup covers this many context
-// tokens (16 pages of 16 tokens).
-constexpr uint32_t kAttnSplitTokens = 256;
+// Attention partition: each partition workgroup covers this many pages of
+// 16 tokens (8 per wave).
+constexpr uint32_t kAttnSplitPages = 32;
+constexpr uint32_t kAttnSplitTokens = kAttnSplitPages * 16;
 // Floats per attention partial record: running max, denominator, numerator[128].
 constexpr uint32_t kAttnPartialFloats = 2 + 128;
 // Argmax first-pass shards per row.
 constexpr uint32_t kArgmaxShards = 64;
+// Token rows of one decode step (the activation tile order holds 2 m-tiles);
+// split-K partial slabs are [kMaxRows][n] FP32.
+constexpr uint32_t kMaxRows = 32;
 
 inline uint32_t attn_max_splits(uint32_t context_tokens) {
   return (context_tokens + kAttnSplitTokens - 1) / kAttnSplitTokens;
@@ -36,25 +40,35 @@ hipError_t launch_copy_u16(const uint16_t* src, uint16_t* dst, uint64_t count, h
 // norms / activation
 hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, uint32_t rows, uint32_t width,
                           float eps, uint32_t* err, hipStream_t s);
-hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
-                                 const float* cos_t, const float* sin_t, const uint32_t* positions,
-                                 const uint32_t* table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
-                                 uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
-                                 uint32_t context, float eps, uint32_t* err, hipStream_t s);
+hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uint32_t splits, const uint16_t* q_norm,
+                                 const uint16_t* k_norm, const float* cos_t, const float* sin_t,
+                                 const uint32_t* positions, const uint32_t* table, uint16_t* q_out,
+                                 uint16_t* k_cache, uint16_t* v_cache, uint32_t rows, uint32_t qh, uint32_t kvh,
+                                 uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err,
+                                 hipStream_t s);
+hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* w,
+                                   uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float eps,
+                                   uint32_t* err, hipStream_t s);
+hipError_t launch_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, uint32_t to_tiled,
+                                  hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t n, uint32_t* err,
                          hipStream_t s);
 
 // projections
-hipError_t launch_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
-                       uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s);
+hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
+                       hipStream_t s);
+uint32_t gemm_default_splits(uint32_t n, uint32_t k);
 
 // attention
+// out: [rows][qh*128] row-major, or activation tile order when out_tiled.
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                    const uint32_t* positions, const uint32_t* table, float* partials, uint32_t rows,
-                                    uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                                    uint32_t* err, hipStream_t s);
-hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out, uint32_t rows,
-                                  uint32_t qh, uint32_t context, uint32_t* err, hipStream_t s);
+                                    const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
+                                    uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride,
+                                    uint32_t pages, uint32_t context, uint32_t* err, hipStream_t s);
+hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
+                                  uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t context, uint32_t* err,
+                                  hipStream_t s);
 
 // logits
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,

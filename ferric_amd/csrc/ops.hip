@@ -50,33 +50,60 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
   return from_hip(fh::launch_rmsnorm(x, weight, y, rows, width, epsilon, error_word, as_stream(stream)));
 }
 
-fh_status fh_op_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
-                     uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, void* stream) {
-  if (!x || !w_tiled || !out || m == 0 || m > 32 || n == 0 || k == 0 || n % 16 || k % 32 || ldx < k || ldx % 8)
+fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                     uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
+                     void* stream) {
+  if (!x_tiled || !w_tiled || !out || m == 0 || m > fh::kMaxRows || n == 0 || k == 0 || n % 16 || k % 32)
     return FH_ERR_INVALID_ARGUMENT;
-  if (epilogue > FH_EPI_F32) return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue > FH_EPI_PARTIAL || splits == 0 || splits > k / 32) return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue != FH_EPI_PARTIAL && splits != 1) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue == FH_EPI_RESIDUAL && !residual) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue == FH_EPI_SWIGLU) {
-    if (n % 32 || ldo < n / 2) return FH_ERR_INVALID_ARGUMENT;
+    if (n % 32) return FH_ERR_INVALID_ARGUMENT;  // the output is in activation tile order
   } else if (ldo < n) {
     return FH_ERR_INVALID_ARGUMENT;
   }
-  return from_hip(fh::launch_gemm(x, ldx, w_tiled, m, n, k, epilogue, residual, out, ldo, as_stream(stream)));
+  return from_hip(fh::launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, splits, residual, out, ldo, as_stream(stream)));
 }
 
-fh_status fh_op_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k) { return fh::gemm_default_splits(n, k); }
+
+fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream) {
+  if (!x || !x_tiled || m == 0 || m > fh::kMaxRows || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_tile_activation(x, x_tiled, m, k, 1, as_stream(stream)));
+}
+
+fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t m, uint32_t k, void* stream) {
+  if (!x || !x_tiled || m == 0 || m > fh::kMaxRows || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_tile_activation(x, const_cast<uint16_t*>(x_tiled), m, k, 0, as_stream(stream)));
+}
+
+fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* weight,
+                                 uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float epsilon,
+                                 uint32_t* error_word, void* stream) {
+  if (!hidden || !weight || !y || rows == 0 || width == 0 || width % 32 || width > 8192 || (splits && !partials))
+    return FH_ERR_INVALID_ARGUMENT;
+  if (y_tiled && rows > fh::kMaxRows) return FH_ERR_INVALID_ARGUMENT;
+  if (splits && rows > fh::kMaxRows) return FH_ERR_INVALID_ARGUMENT;
+  return from_hip(fh::launch_residual_rmsnorm(hidden, partials, splits, weight, y, y_tiled, rows, width, epsilon,
+                                              error_word, as_stream(stream)));
+}
+
+fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint16_t* q_norm, const uint16_t* k_norm,
                                const float* cos_table, const float* sin_table, const uint32_t* positions,
                                const uint32_t* page_table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
                                uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
                                uint32_t physical_pages, uint32_t context_tokens, float epsilon, uint32_t* error_word,
                                void* stream) {
   if (!qkv || !q_norm || !k_norm || !cos_table || !sin_table || !positions || !page_table || !q_out || !k_cache ||
-      !v_cache || rows == 0 || query_heads == 0 || kv_heads == 0 || query_heads + kv_heads > 64 || stride == 0 ||
-      physical_pages == 0 || context_tokens == 0)
+      !v_cache || rows == 0 || query_heads == 0 || kv_heads == 0 || query_heads + 2 * kv_heads > 64 || stride == 0 ||
+      physical_pages == 0 || context_tokens == 0 || (qkv_splits && rows > fh::kMaxRows))
     return FH_ERR_INVALID_ARGUMENT;
-  return from_hip(fh::launch_qknorm_rope_kv(qkv, q_norm, k_norm, cos_table, sin_table, positions, page_table, q_out,
-                                            k_cache, v_cache, rows, query_heads, kv_heads, stride, physical_pages,
-                                            context_tokens, epsilon, error_word, as_stream(stream)));
+  const uint16_t* bf = qkv_splits ? nullptr : reinterpret_cast<const uint16_t*>(qkv);
+  const float* part = qkv_splits ? reinterpret_cast<const float*>(qkv) : nullptr;
+  return from_hip(fh::launch_qknorm_rope_kv(bf, part, qkv_splits, q_norm, k_norm, cos_table, sin_table, positions,
+                                            page_table, q_out, k_cache, v_cache, rows, query_heads, kv_heads, stride,
+                                            physical_pages, context_tokens, epsilon, error_word, as_stream(stream)));
 }
 
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens) {
@@ -84,22 +111,23 @@ uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_
 }
 
 fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                const uint32_t* positions, const uint32_t* page_table, uint16_t* out, void* scratch,
-                                uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
-                                uint32_t physical_pages, uint32_t context_tokens, uint32_t* error_word,
-                                void* stream) {
+                                const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
+                                uint32_t out_tiled, void* scratch, uint32_t rows, uint32_t query_heads,
+                                uint32_t kv_heads, uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
+                                uint32_t* error_word, void* stream) {
   if (!q || !k_cache || !v_cache || !positions || !page_table || !out || !scratch || rows == 0 || kv_heads == 0 ||
       query_heads % kv_heads != 0 || stride == 0 || physical_pages == 0 || context_tokens == 0 ||
-      (uint64_t)stride * 16 < context_tokens)
+      (uint64_t)stride * 16 < context_tokens || (out_tiled && rows > fh::kMaxRows))
     return FH_ERR_INVALID_ARGUMENT;
   const uint32_t g = query_heads / kv_heads;
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
   hipStream_t s = as_stream(stream);
   float* part = reinterpret_cast<float*>(scratch);
-  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, rows, query_heads,
-                                              kv_heads, stride, physical_pages, context_tokens, error_word, s);
-  if (e == hipSuccess) e = fh::launch_attention_merge(part, positions, out, rows, query_heads, context_tokens,
-                                                      error_word, s);
+  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, rows,
+                                              query_heads, kv_heads, stride, physical_pages, context_tokens,
+                                              error_word, s);
+  if (e == hipSuccess)
+    e = fh::launch_attention_merge(part, positions, out, out_tiled, rows, query_heads, context_tokens, error_word, s);
   return from_hip(e);
 }
 

@@ -66,12 +66,15 @@ struct fh_ctx {
   float* cos_t = nullptr;
   float* sin_t = nullptr;
 
-  uint16_t* hidden = nullptr;
-  uint16_t* xn = nullptr;
-  uint16_t* qkv = nullptr;
-  uint16_t* qrot = nullptr;
-  uint16_t* attn = nullptr;
-  uint16_t* act = nullptr;
+  uint16_t* hidden = nullptr;  // residual stream, row-major [cap][hidden]
+  uint16_t* xn = nullptr;      // normalized rows, activation tile order
+  uint16_t* qrot = nullptr;    // rotated queries, row-major [cap][qh*128]
+  uint16_t* attn = nullptr;    // attention output, activation tile order
+  uint16_t* act = nullptr;     // SwiGLU output, activation tile order
+  float* qkv_part = nullptr;   // split-K partial slabs [s_qkv][32][nqkv]
+  float* o_part = nullptr;     // [s_o][32][hidden]
+  float* down_part = nullptr;  // [s_down][32][hidden]
+  uint32_t s_qkv = 1, s_o = 1, s_down = 1;
   float* logits = nullptr;
   float* attn_part = nullptr;
   void* argmax_scratch = nullptr;
@@ -345,45 +348,66 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
     q.run(cls, f);
     ++n;
   };
+  // Residual stream: `hidden` (row-major bf16). Projection inputs (xn, attn,
+  // act) are in activation tile order. The O and down projections leave
+  // split-K FP32 partials that the next residual + RMSNorm folds into
+  // `hidden` (one rounding, as the TP1 residual); the QKV partials are folded
+  // by the QK-norm kernel.
+  const uint32_t sq = ctx->s_qkv, so = ctx->s_o, sd = ctx->s_down;
   L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, ctx->hidden, R, H, md.vocabulary, err, s); });
   for (uint32_t l = 0; l < md.layers; ++l) {
     const LayerWeights& W = ctx->layers[l];
     uint16_t* kc = kv_cache(ctx, l, 0);
     uint16_t* vc = kv_cache(ctx, l, 1);
-    L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, W.in_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+    const uint32_t fold = l == 0 ? 0 : sd;
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, fold, W.in_norm, ctx->xn, 1, R, H,
+                                         md.rms_epsilon, err, s);
+    });
+    if (ctx->capture && l > 0)
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(l - 1) * cap * H, (uint64_t)R * H, s);
+      });
     L(FH_KC_QKV_GEMM, [&] {
-      return fh::launch_gemm(ctx->xn, H, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, ctx->qkv, ctx->nqkv, s);
+      return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part, ctx->nqkv,
+                             s);
     });
     L(FH_KC_QKNORM_ROPE_KV, [&] {
-      return fh::launch_qknorm_rope_kv(ctx->qkv, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, ctx->qrot,
-                                       kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon, err, s);
+      return fh::launch_qknorm_rope_kv(nullptr, ctx->qkv_part, sq, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos,
+                                       d_tab, ctx->qrot, kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon, err, s);
     });
     L(FH_KC_ATTENTION, [&] {
-      return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, R, QH, KVH, stride, P, C,
-                                          err, s);
+      return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, ctx->attn, 1, R, QH, KVH,
+                                          stride, P, C, err, s);
     });
     L(FH_KC_ATTENTION_MERGE, [&] {
-      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, R, QH, C, err, s);
+      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, R, QH, C, err, s);
     });
     L(FH_KC_O_GEMM, [&] {
-      return fh::launch_gemm(ctx->attn, Q, W.o, R, H, Q, FH_EPI_RESIDUAL, ctx->hidden, ctx->hidden, H, s);
+      return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, s);
     });
-    L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, W.post_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(ctx->hidden, ctx->o_part, so, W.post_norm, ctx->xn, 1, R, H, md.rms_epsilon,
+                                         err, s);
+    });
     L(FH_KC_GATE_UP_GEMM, [&] {
-      return fh::launch_gemm(ctx->xn, H, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, ctx->act, I, s);
+      return fh::launch_gemm(ctx->xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, 1, nullptr, ctx->act, I, s);
     });
     L(FH_KC_DOWN_GEMM, [&] {
-      return fh::launch_gemm(ctx->act, I, W.down, R, H, I, FH_EPI_RESIDUAL, ctx->hidden, ctx->hidden, H, s);
+      return fh::launch_gemm(ctx->act, W.down, R, H, I, FH_EPI_PARTIAL, sd, nullptr, ctx->down_part, H, s);
     });
-    if (ctx->capture)
-      L(FH_KC_RMSNORM, [&] {
-        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)l * cap * H, (uint64_t)R * H, s);
-      });
   }
-  L(FH_KC_RMSNORM, [&] { return fh::launch_rmsnorm(ctx->hidden, ctx->final_norm, ctx->xn, R, H, md.rms_epsilon, err, s); });
+  L(FH_KC_RMSNORM, [&] {
+    return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, sd, ctx->final_norm, ctx->xn, 1, R, H,
+                                       md.rms_epsilon, err, s);
+  });
+  if (ctx->capture)
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(md.layers - 1) * cap * H, (uint64_t)R * H, s);
+    });
   L(FH_KC_HEAD_GEMM, [&] {
-    return fh::launch_gemm(ctx->xn, H, ctx->head, R, md.vocabulary, H, FH_EPI_F32, nullptr, ctx->logits,
+    return fh::launch_gemm(ctx->xn, ctx->head, R, md.vocabulary, H, FH_EPI_F32, 1, nullptr, ctx->logits,
                            md.vocabulary, s);
   });
   L(FH_KC_ARGMAX, [&] {
@@ -472,11 +496,17 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   TRY(dalloc(ctx, &ctx->cos_t, (uint64_t)op.context_tokens * 64));
   TRY(dalloc(ctx, &ctx->sin_t, (uint64_t)op.context_tokens * 64));
   TRY(dalloc(ctx, &ctx->hidden, (uint64_t)cap * H));
-  TRY(dalloc(ctx, &ctx->xn, (uint64_t)cap * H));
-  TRY(dalloc(ctx, &ctx->qkv, (uint64_t)cap * ctx->nqkv));
+  // Activation-tile buffers always hold 32 rows (two 16-row m-tiles).
+  TRY(dalloc(ctx, &ctx->xn, (uint64_t)kMaxRows * H));
   TRY(dalloc(ctx, &ctx->qrot, (uint64_t)cap * Q));
-  TRY(dalloc(ctx, &ctx->attn, (uint64_t)cap * Q));
-  TRY(dalloc(ctx, &ctx->act, (uint64_t)cap * I));
+  TRY(dalloc(ctx, &ctx->attn, (uint64_t)kMaxRows * Q));
+  TRY(dalloc(ctx, &ctx->act, (uint64_t)kMaxRows * I));
+  ctx->s_qkv = fh::gemm_default_splits(ctx->nqkv, H);
+  ctx->s_o = fh::gemm_default_splits(H, Q);
+  ctx->s_down = fh::gemm_default_splits(H, I);
+  TRY(dalloc(ctx, &ctx->qkv_part, (uint64_t)ctx->s_qkv * kMaxRows * ctx->nqkv));
+  TRY(dalloc(ctx, &ctx->o_part, (uint64_t)ctx->s_o * kMaxRows * H));
+  TRY(dalloc(ctx, &ctx->down_part, (uint64_t)ctx->s_down * kMaxRows * H));
   TRY(dalloc(ctx, &ctx->logits, (uint64_t)cap * V));
   TRY(dalloc(ctx, &ctx->attn_part,
              (uint64_t)cap * md.query_heads * fh::attn_max_splits(op.context_tokens) * fh::kAttnPartialFloats));

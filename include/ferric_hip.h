@@ -207,31 +207,52 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
  * FH_EPI_F32 (FP32 out, the LM head). m <= 32. Replaces gemm.rs:161/:605 and
  * device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15/:142/:241, collective.rs:25,
  * activation.rs:32 and device/qwen3-tp-fp32-head32-kernels-v8/src/projection.rs:66/:186. */
-enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3 };
-fh_status fh_op_gemm(const uint16_t* x, uint32_t ldx, const uint16_t* w_tiled, uint32_t m, uint32_t n,
-                     uint32_t k, uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo,
+enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3, FH_EPI_PARTIAL = 4 };
+/* x_tiled is in activation tile order (fh_op_tile_activation). FH_EPI_SWIGLU writes its
+ * output in activation tile order (the down projection's input); FH_EPI_PARTIAL writes
+ * FP32 partial sums as `splits` slabs of [32][ldo] (split-K across workgroups; the
+ * consumer adds the slabs in order and rounds once). Other epilogues use splits = 1. */
+fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                     uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                      void* stream);
+/* Split-K factor the runtime uses for an n x k projection. */
+uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k);
+/* Row-major [m][k] bf16 <-> activation tile order (m <= 32; the tiled buffer holds 32 x k). */
+fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream);
+fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t m, uint32_t k, void* stream);
+
+/* K2 residual + RMSNorm, fused: when splits > 0, hidden[r] = bf16((0 + sum_s partials[s][r]) +
+ * hidden[r]) is written back first (the TP1 residual, v5 collective.rs:25-60, with the split-K
+ * slabs summed in order), then y = RMSNorm(hidden) is written in activation tile order
+ * (y_tiled = 1) or row-major. partials: `splits` slabs of [32][width] FP32. */
+fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* weight,
+                                 uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float epsilon,
+                                 uint32_t* error_word, void* stream);
 
 /* K3 per-head QK-norm + split-half RoPE + paged KV append, one launch.
- * qkv: [rows][(qh + 2*kvh) * 128] projection output; q_out: [rows][qh*128] rotated queries;
+ * qkv: [rows][(qh + 2*kvh) * 128] bf16 projection output when qkv_splits == 0, else
+ * qkv_splits FP32 partial slabs of [32][(qh + 2*kvh) * 128] (each value = bf16 of the ordered
+ * slab sum); q_out: [rows][qh*128] rotated queries;
  * k_cache/v_cache: [pages][16][kvh][128]; cos/sin: [context][64] f32 table;
  * page_table: [rows][stride]. Replaces qwen3_rmsnorm_v1 at width 128 (batched.rs:1956-1982),
  * qwen3_rope_v1 (rope_kv.rs:102) and qwen3_paged_kv_write_v1 (rope_kv.rs:261). */
-fh_status fh_op_qknorm_rope_kv(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm,
+fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint16_t* q_norm, const uint16_t* k_norm,
                                const float* cos_table, const float* sin_table, const uint32_t* positions,
                                const uint32_t* page_table, uint16_t* q_out, uint16_t* k_cache,
                                uint16_t* v_cache, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
                                uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
                                float epsilon, uint32_t* error_word, void* stream);
 
-/* K4 paged GQA decode attention: split-context partials then an ordered merge.
- * q: [rows][qh*128]; out: [rows][qh*128] bf16; scratch: fh_attention_scratch_bytes().
+/* K4 paged GQA decode attention: split-context partitions then an ordered merge.
+ * q: [rows][qh*128]; out: [rows][qh*128] bf16 row-major, or activation tile order when
+ * out_tiled (the output projection's input); scratch: fh_attention_scratch_bytes().
  * Replaces qwen3_paged_gqa_decode_bf16_f32_v1 (paged_decode.rs:222) and the split8
  * partial/merge pair (device/qwen3-tp-c1-split8-attention-kernels-v21/src/attention.rs:16, :214). */
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens);
 fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                 const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
-                                void* scratch, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                                uint32_t out_tiled, void* scratch, uint32_t rows, uint32_t query_heads,
+                                uint32_t kv_heads,
                                 uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
                                 uint32_t* error_word, void* stream);
 

@@ -651,6 +651,25 @@ int orc_model_forward(OrcModel* m, const uint32_t* tokens, const uint32_t* posit
 }
 
 
+// Final RMSNorm + FP32 LM head + argmax from a caller-given residual stream
+// hidden_in [rows][hidden] (the head's own error on the GPU's final hidden
+// state). Returns 0, or 1 where the reference traps.
+int orc_model_head(OrcModel* m, const uint16_t* hidden_in, uint32_t rows, float* logits, uint32_t* choices,
+                   float* gaps) {
+  const uint32_t H = m->hidden, V = m->vocab;
+  std::vector<uint16_t> xn((uint64_t)rows * H);
+  if (orc_rmsnorm(hidden_in, nullptr, m->final_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
+  orc_gemm(xn.data(), m->tied ? m->embed.data() : m->head.data(), nullptr, rows, V, H, 0, nullptr, logits);
+  for (uint32_t r = 0; r < rows; ++r) {
+    float gap = 0.f;
+    const uint32_t c = orc_argmax_f32(logits + (uint64_t)r * V, V, &gap);
+    if (c == 0xffffffffu) return 1;
+    choices[r] = c;
+    if (gaps) gaps[r] = gap;
+  }
+  return 0;
+}
+
 // Layer `layer` alone, from a caller-given input residual stream hidden_in
 // [rows][hidden] to hidden_out, against a scratch copy of that layer's KV
 // (the model's pool is left untouched). Used to measure one layer's numerical

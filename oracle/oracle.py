@@ -99,6 +99,8 @@ def lib():
         L.orc_model_layer_isolated.argtypes = [ctypes.c_void_p, _c_u32, _u16p, _u32p, _u32p, _u32p, _c_u32, _c_u32,
                                                _u16p]
         L.orc_model_layer_isolated.restype = ctypes.c_int
+        L.orc_model_head.argtypes = [ctypes.c_void_p, _u16p, _c_u32, _f32p, _u32p, _f32p]
+        L.orc_model_head.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -331,6 +333,19 @@ class Model:
         if st:
             raise RuntimeError("oracle layer trapped")
         return out.reshape(len(positions), -1)
+
+    def head(self, hidden_in):
+        """Final RMSNorm + FP32 head + argmax on a given residual stream."""
+        hidden_in = np.ascontiguousarray(hidden_in, np.uint16)
+        rows = hidden_in.size // self.desc["hidden"]
+        logits = np.zeros(rows * self.desc["vocabulary"], np.float32)
+        choices = np.zeros(rows, np.uint32)
+        gaps = np.zeros(rows, np.float32)
+        st = lib().orc_model_head(self.h, _ptr(hidden_in.reshape(-1), _u16p), rows, _ptr(logits, _f32p),
+                                  _ptr(choices, _u32p), _ptr(gaps, _f32p))
+        if st:
+            raise RuntimeError("oracle head trapped")
+        return {"logits": logits.reshape(rows, -1), "choices": choices, "gaps": gaps}
 
     def forward(self, tokens, positions, tables, page_counts, stride, want_logits=True, want_hidden=False):
         d = self.desc

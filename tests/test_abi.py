@@ -78,24 +78,33 @@ def test_token_assembly_matches_the_oracle():
 
 def test_scratch_sizes():
     lib = ferric_amd.load()
-    # 32 rows x 32 heads x ceil(8320 / 256) partitions x (2 + 128) f32
-    assert lib.fh_attention_scratch_bytes(32, 32, 8320) == 32 * 32 * 33 * 130 * 4
+    # 32 rows x 32 heads x ceil(8320 / 512) partitions x (2 + 128) f32
+    assert lib.fh_attention_scratch_bytes(32, 32, 8320) == 32 * 32 * 17 * 130 * 4
     assert lib.fh_argmax_scratch_bytes(32) == 32 * 64 * 8
+    # split-K factors keep about 512 workgroups per projection launch
+    assert lib.fh_gemm_default_splits(6144, 4096) >= 4
+    assert lib.fh_gemm_default_splits(24576, 4096) == 2
+    assert lib.fh_gemm_default_splits(151936, 4096) == 1
 
 
 def test_ops_reject_bad_shapes_before_any_launch():
     lib = ferric_amd.load()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    assert lib.fh_op_gemm(p, 64, p, 0, 64, 64, 0, None, p, 64, None) == 1  # m = 0
-    assert lib.fh_op_gemm(p, 64, p, 33, 64, 64, 0, None, p, 64, None) == 1  # m > 32
-    assert lib.fh_op_gemm(p, 64, p, 4, 60, 64, 0, None, p, 64, None) == 1  # n % 16
-    assert lib.fh_op_gemm(p, 64, p, 4, 64, 48, 0, None, p, 64, None) == 1  # k % 32
-    assert lib.fh_op_gemm(p, 64, p, 4, 64, 64, 1, None, p, 64, None) == 1  # residual epilogue without residual
-    assert lib.fh_op_gemm(p, 64, p, 4, 64, 64, 9, None, p, 64, None) == 1  # unknown epilogue
+    assert lib.fh_op_gemm(p, p, 0, 64, 64, 0, 1, None, p, 64, None) == 1  # m = 0
+    assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None) == 1  # m > 32
+    assert lib.fh_op_gemm(p, p, 4, 60, 64, 0, 1, None, p, 64, None) == 1  # n % 16
+    assert lib.fh_op_gemm(p, p, 4, 64, 48, 0, 1, None, p, 64, None) == 1  # k % 32
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 1, 1, None, p, 64, None) == 1  # residual epilogue without residual
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 9, 1, None, p, 64, None) == 1  # unknown epilogue
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 0, 2, None, p, 64, None) == 1  # splits on a non-partial epilogue
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 4, 3, None, p, 64, None) == 1  # more splits than k-blocks
     assert lib.fh_op_tile_weight(p, p, 17, 32, None) == 1
+    assert lib.fh_op_tile_activation(p, p, 33, 64, None) == 1
     assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1
-    assert lib.fh_op_paged_attention(p, p, p, p, p, p, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
-    assert lib.fh_op_paged_attention(p, p, p, p, p, p, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
+    assert lib.fh_op_residual_rmsnorm(p, None, 2, p, p, 1, 4, 4096, 1e-6, None, None) == 1  # partials missing
+    assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
+    assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
+    assert lib.fh_op_paged_attention(p, p, p, p, p, p, 1, p, 40, 32, 8, 4, 4, 64, None, None) == 1  # tiled > 32 rows
 
 
 def test_create_rejects_unsupported_shapes_without_touching_the_device():

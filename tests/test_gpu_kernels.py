@@ -120,49 +120,96 @@ def test_rmsnorm_known_answers():
         assert du.to_host(err, np.uint32)[0] != 0
 
 
-def _gemm_case(m, n, k, epi, seed):
+def act_tile_host(x, m, k):
+    """Numpy statement of the activation tile order for x[m][k] (m <= 32):
+    tile (kb, mt) = rows 16 mt.., cols 32 kb..; lane = row % 16 + 16 * ((col % 32) // 8)."""
+    full = np.zeros((32, k), np.uint16)
+    full[:m] = x.reshape(m, k)
+    t = full.reshape(2, 16, k // 32, 4, 8)  # mt, r, kb, g, e
+    t = t.transpose(2, 0, 3, 1, 4)  # kb, mt, g, r, e -> lane = g*16 + r
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def to_tiled_act(x, m, k):
+    dx = du.to_dev(x)
+    dxt = du.empty(32 * k, np.uint16)
+    _lib.check(LIB.fh_op_tile_activation(du.ptr(dx), du.ptr(dxt), m, k, du.stream()))
+    return dxt
+
+
+def test_activation_tile_order_round_trip():
+    r = rng(8)
+    for m, k in [(1, 32), (7, 64), (16, 1024), (17, 96), (32, 4096)]:
+        x = r.integers(0, 65536, m * k, dtype=np.uint64).astype(np.uint16)
+        dxt = to_tiled_act(x, m, k)  # rows >= m stay zero (never written)
+        assert np.array_equal(du.to_host(dxt, np.uint16), act_tile_host(x, m, k)), (m, k)
+        back = du.empty(m * k, np.uint16)
+        _lib.check(LIB.fh_op_untile_activation(du.ptr(dxt), du.ptr(back), m, k, du.stream()))
+        assert np.array_equal(du.to_host(back, np.uint16), x)
+
+
+def _gemm_case(m, n, k, epi, seed, splits=1):
     r = rng(seed)
     x = rand_bf16(r, m * k, 1.0)
     w = rand_bf16(r, n * k, 0.02)
-    dx, dw_ = du.to_dev(x), du.to_dev(w)
+    dxt = to_tiled_act(x, m, k)
+    dw_ = du.to_dev(w)
     dt = du.empty(n * k, np.uint16)
     if epi == _lib.EPI_SWIGLU:
         i = n // 2
         gate, up = w[: i * k], w[i * k:]
         dg, du_ = du.to_dev(gate), du.to_dev(up)
         _lib.check(LIB.fh_op_tile_gate_up(du.ptr(dg), du.ptr(du_), du.ptr(dt), i, k, du.stream()))
+        out_t = du.empty(32 * i, np.uint16)  # activation tile order (the down projection's input)
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out_t), i, du.stream()))
         out = du.empty(m * i, np.uint16)
-        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), i, du.stream()))
+        _lib.check(LIB.fh_op_untile_activation(du.ptr(out_t), du.ptr(out), m, i, du.stream()))
         got = du.to_host(out, np.uint16)
         g = orc.gemm(x, gate, m, i, k)
         u = orc.gemm(x, up, m, i, k)
         return got, orc.swiglu(g, u)
     _lib.check(LIB.fh_op_tile_weight(du.ptr(dw_), du.ptr(dt), n, k, du.stream()))
+    if epi == _lib.EPI_PARTIAL:
+        out = du.empty(splits * 32 * n, np.float32)
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, splits, None, du.ptr(out), n, du.stream()))
+        slabs = du.to_host(out, np.float32).reshape(splits, 32, n)[:, :m]
+        total = slabs[0].copy()
+        for sp in range(1, splits):
+            total = (total + slabs[sp]).astype(np.float32)
+        return total.reshape(-1), orc.gemm(x, w, m, n, k, f32_out=True)
     if epi == _lib.EPI_F32:
         out = du.empty(m * n, np.float32)
-        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), n, du.stream()))
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, du.stream()))
         return du.to_host(out, np.float32), orc.gemm(x, w, m, n, k, f32_out=True)
     if epi == _lib.EPI_RESIDUAL:
         res = rand_bf16(r, m * n, 1.0)
-        out = du.to_dev(res)  # in place, as the runtime uses it
-        _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, du.ptr(out), du.ptr(out), n, du.stream()))
+        out = du.to_dev(res)  # in place
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, du.ptr(out), du.ptr(out), n, du.stream()))
         part = orc.gemm(x, w, m, n, k, f32_out=True)
         return du.to_host(out, np.uint16), orc.residual(part, res)
     out = du.empty(m * n, np.uint16)
-    _lib.check(LIB.fh_op_gemm(du.ptr(dx), k, du.ptr(dt), m, n, k, epi, None, du.ptr(out), n, du.stream()))
+    _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, du.stream()))
     return du.to_host(out, np.uint16), orc.gemm(x, w, m, n, k)
 
 
+F32_BOUND = 1.6e-4  # FP32 reassociation of <= 12288 products of |x| ~ 1, |w| ~ 0.02
+
+
 @pytest.mark.parametrize("m", [1, 7, 16, 17, 32])
-@pytest.mark.parametrize("n,k", [(64, 64), (256, 1024), (1024, 4096), (512, 12288)])
+@pytest.mark.parametrize("n,k", [(64, 64), (256, 1024), (1024, 4096), (512, 12288), (48, 128)])
 def test_gemm_bf16_and_f32_epilogues(m, n, k):
     got, ref = _gemm_case(m, n, k, _lib.EPI_F32, m * 7 + n)
-    # FP32 reassociation only: |error| is a few f32 ulps of the partial sums.
-    scale = np.sqrt(k) * 0.02
-    assert np.max(np.abs(got - ref)) <= 2e-5 * scale * 8
+    assert np.max(np.abs(got - ref)) <= F32_BOUND
     got, ref = _gemm_case(m, n, k, _lib.EPI_BF16, m * 7 + n + 1)
     assert du.bf16_close(got, ref, ulps=1)
     assert np.mean(got == ref) > 0.99
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(32, 6144, 4096, 6), (32, 4096, 12288, 8), (5, 1024, 1024, 2),
+                                          (17, 256, 4096, 3), (32, 64, 128, 4)])
+def test_gemm_split_k_partials(m, n, k, splits):
+    got, ref = _gemm_case(m, n, k, _lib.EPI_PARTIAL, 31 * m + splits, splits=splits)
+    assert np.max(np.abs(got - ref)) <= F32_BOUND
 
 
 @pytest.mark.parametrize("m", [3, 32])
@@ -170,12 +217,43 @@ def test_gemm_residual_and_swiglu_epilogues(m):
     got, ref = _gemm_case(m, 512, 4096, _lib.EPI_RESIDUAL, 99 + m)
     assert du.bf16_close(got, ref, ulps=1)
     assert np.mean(got == ref) > 0.99
-    got, ref = _gemm_case(m, 1024, 1024, _lib.EPI_SWIGLU, 199 + m)
-    assert ref is not None
-    # gate and up are each one bf16 rounding of a reassociated sum (<= 1 ulp),
-    # and SwiGLU multiplies them: <= 2 ulps of the product, plus exp's last ulp.
-    assert du.bf16_close(got, ref, ulps=3)
-    assert np.mean(got == ref) > 0.97
+    for n in (1024, 6144):
+        got, ref = _gemm_case(m, n, 1024, _lib.EPI_SWIGLU, 199 + m + n)
+        assert ref is not None
+        # gate and up are each one bf16 rounding of a reassociated sum (<= 1 ulp),
+        # and SwiGLU multiplies them: <= 2 ulps of the product, plus exp's last ulp.
+        assert du.bf16_close(got, ref, ulps=3)
+        assert np.mean(got == ref) > 0.97
+
+
+@pytest.mark.parametrize("splits", [0, 1, 3])
+@pytest.mark.parametrize("rows,width", [(1, 1024), (32, 4096), (9, 4096)])
+def test_residual_rmsnorm(splits, rows, width):
+    r = rng(splits * 100 + rows)
+    hidden = rand_bf16(r, rows * width, 2.0)
+    w = rand_bf16(r, width, 1.0)
+    slabs = (r.standard_normal((max(splits, 1), 32, width)) * 0.5).astype(np.float32)
+    dh, dw_, dp = du.to_dev(hidden), du.to_dev(w), du.to_dev(slabs.reshape(-1))
+    dy = du.empty(32 * width, np.uint16)
+    err = du.empty(1, np.uint32)
+    _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp) if splits else None, splits, du.ptr(dw_), du.ptr(dy),
+                                          1, rows, width, 1e-6, du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    new_h = du.to_host(dh, np.uint16)
+    if splits:
+        total = slabs[0, :rows].copy()
+        for sp in range(1, splits):
+            total = (total + slabs[sp, :rows]).astype(np.float32)
+        exp_h = orc.residual(total.reshape(-1), hidden)  # bf16((0 + P) + h): bit-exact
+    else:
+        exp_h = hidden
+    assert np.array_equal(new_h, exp_h)
+    y = du.empty(rows * width, np.uint16)
+    _lib.check(LIB.fh_op_untile_activation(du.ptr(dy), du.ptr(y), rows, width, du.stream()))
+    got = du.to_host(y, np.uint16)
+    ref = orc.rmsnorm(exp_h, w, rows, width)
+    assert du.bf16_ulp_diff(got, ref) <= 2
+    assert np.mean(got == ref) > 0.99
 
 
 def _paged_pool(r, pages, kvh, scale=1.0):
@@ -183,9 +261,9 @@ def _paged_pool(r, pages, kvh, scale=1.0):
     return rand_bf16(r, n, scale), rand_bf16(r, n, scale)
 
 
-@pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
-def test_qknorm_rope_kv_bit_exact(qh, kvh):
-    r = rng(qh)
+@pytest.mark.parametrize("qh,kvh,splits", [(32, 8, 0), (16, 8, 0), (32, 8, 1), (32, 8, 3)])
+def test_qknorm_rope_kv_bit_exact(qh, kvh, splits):
+    r = rng(qh + splits)
     rows, pages, stride, context = 9, 64, 64, 1024
     ld = (qh + 2 * kvh) * 128
     qkv = rand_bf16(r, rows * ld, 2.0)
@@ -204,9 +282,24 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh):
     dkc, dvc = du.to_dev(kc0), du.to_dev(vc0)
     dq = du.empty(rows * qh * 128, np.uint16)
     err = du.empty(1, np.uint32)
-    keep = [du.to_dev(a) for a in (qkv, qn, kn, cos, sin, positions, table)]
-    _lib.check(LIB.fh_op_qknorm_rope_kv(*[du.ptr(t) for t in keep], du.ptr(dq), du.ptr(dkc), du.ptr(dvc), rows, qh,
-                                        kvh, stride, pages, context, 1e-6, du.ptr(err), du.stream()))
+    if splits == 0:
+        src = du.to_dev(qkv)
+    else:
+        # split-K slabs whose ordered f32 sum is exactly the bf16 value:
+        # slab 0 = 2 v, slab 1 = -v (2v - v is exact), rest 0.
+        vals = orc.bf16_to_f32(qkv).reshape(rows, ld)
+        slabs = np.zeros((splits, 32, ld), np.float32)
+        if splits == 1:
+            slabs[0, :rows] = vals
+        else:
+            slabs[0, :rows] = vals * np.float32(2.0)
+            slabs[1, :rows] = -vals
+        assert np.array_equal(((slabs[0, :rows] + (slabs[1, :rows] if splits > 1 else 0))).astype(np.float32), vals)
+        src = du.to_dev(slabs.reshape(-1))
+    keep = [du.to_dev(a) for a in (qn, kn, cos, sin, positions, table)]
+    _lib.check(LIB.fh_op_qknorm_rope_kv(du.ptr(src), splits, *[du.ptr(t) for t in keep], du.ptr(dq), du.ptr(dkc),
+                                        du.ptr(dvc), rows, qh, kvh, stride, pages, context, 1e-6, du.ptr(err),
+                                        du.stream()))
     assert du.to_host(err, np.uint32)[0] == 0
     got_q = du.to_host(dq, np.uint16).reshape(rows, qh * 128)
     got_k = du.to_host(dkc, np.uint16)
@@ -220,10 +313,11 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh):
         c, s = orc.rope_table(int(positions[i]))
         qr = np.zeros_like(q)
         kr = np.zeros_like(k)
-        for src, dst, heads in [(q, qr, qh), (k, kr, kvh)]:
+        for srcv, dst, heads in [(q, qr, qh), (k, kr, kvh)]:
             for h in range(heads):
                 for j in range(64):
-                    a, b = orc.rope_pair(int(src[h * 128 + j]), int(src[h * 128 + j + 64]), float(c[j]), float(s[j]))
+                    a, b = orc.rope_pair(int(srcv[h * 128 + j]), int(srcv[h * 128 + j + 64]), float(c[j]),
+                                         float(s[j]))
                     dst[h * 128 + j], dst[h * 128 + j + 64] = a, b
         assert np.array_equal(got_q[i], qr), f"row {i} rotated q"
         pos = int(positions[i])
@@ -236,23 +330,29 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh):
 
 
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
-def test_paged_attention_within_tolerance(qh, kvh):
+@pytest.mark.parametrize("tiled", [0, 1])
+def test_paged_attention_within_tolerance(qh, kvh, tiled):
     r = rng(1000 + qh)
     pages, stride, context = 600, 520, 8320
-    positions = np.array([0, 15, 16, 255, 256, 257, 1000, 4095, 8319, 77], np.uint32)
+    # one partition (<= 512 tokens), several partitions, page-boundary and partial-page cases
+    positions = np.array([0, 15, 16, 255, 511, 512, 513, 1000, 4095, 8319, 77, 8190, 6000], np.uint32)
     rows = len(positions)
     kc, vc = _paged_pool(r, pages, kvh)
     q = rand_bf16(r, rows * qh * 128, 1.0)
     table = np.stack([r.permutation(pages)[:stride] for _ in range(rows)]).astype(np.uint32)
     scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
-    out = du.empty(rows * qh * 128, np.uint16)
+    out = du.empty((32 if tiled else rows) * qh * 128, np.uint16)
     err = du.empty(1, np.uint32)
     dkc, dvc = du.to_dev(kc), du.to_dev(vc)
     dq, dpos, dtab = du.to_dev(q), du.to_dev(positions), du.to_dev(table)
     _lib.check(LIB.fh_op_paged_attention(du.ptr(dq), du.ptr(dkc), du.ptr(dvc), du.ptr(dpos), du.ptr(dtab),
-                                         du.ptr(out), du.ptr(scratch), rows, qh, kvh, stride, pages, context,
+                                         du.ptr(out), tiled, du.ptr(scratch), rows, qh, kvh, stride, pages, context,
                                          du.ptr(err), du.stream()))
     assert du.to_host(err, np.uint32)[0] == 0
+    if tiled:
+        flat = du.empty(rows * qh * 128, np.uint16)
+        _lib.check(LIB.fh_op_untile_activation(du.ptr(out), du.ptr(flat), rows, qh * 128, du.stream()))
+        out = flat
     got = du.to_host(out, np.uint16).reshape(rows, qh, 128)
     g = qh // kvh
     worst = 0.0
