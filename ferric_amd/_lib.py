@@ -146,6 +146,14 @@ def load() -> ctypes.CDLL:
         return _lib
     if not LIBRARY.exists():
         raise ImportError(f"{LIBRARY} is not built; run `python -m ferric_amd.build` (hipcc, gfx950)")
+    # PyTorch ships its own libamdhip64 under the same soname. Loading torch
+    # first makes this library bind to that copy; the other order maps two
+    # HIP runtimes into the process, and the second one to touch the device
+    # reports that there is none. Without torch the system runtime is used.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(LIBRARY))
     for name, restype, argtypes in SIGNATURES:
         fn = getattr(lib, name)

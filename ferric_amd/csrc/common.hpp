@@ -61,6 +61,11 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Value of lane src (a wave-uniform index), read into every lane.
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
 // ---- MFMA operand types (gfx950 v_mfma_f32_16x16x32_bf16) -----------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -41,10 +41,6 @@ constexpr uint32_t kScaleBits = 0x3db504f3u;  // f32 1/sqrt(128), paged_decode.r
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float lane_bcast(float v, int src) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
-}
-
 // Stores one finished head output (dims 2*lane, 2*lane+1) in either layout.
 __device__ __forceinline__ void store_head(uint16_t* out, bool tiled, uint32_t r, uint32_t qh, uint32_t head, int lane,
                                           uint32_t o0, uint32_t o1) {

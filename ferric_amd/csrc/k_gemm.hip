@@ -190,23 +190,32 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
                        residual, out, ldo);
 }
 
+// Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections):
+// weights of up to 16K rows use NT = 4 (activation traffic half the weight
+// traffic) with 8 waves at k <= 4096 and 4 waves at larger k; wider weights
+// (gate/up, LM head) have enough n-tiles to fill the chip, and NT = 2 keeps
+// twice as many workgroups in flight.
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
-  if (n % 64 == 0)
-    launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
-  else if constexpr (EPI != FH_EPI_SWIGLU)
-    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
-  else
+  if (n % 64 == 0 && n < 16384) {
+    if (k <= 4096)
+      launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    else
+      launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  } else if (n % 32 == 0) {
     launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  } else if constexpr (EPI != FH_EPI_SWIGLU) {
+    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  }
 }
 
-// Splits so that a launch has about 512 workgroups, each split keeping at
-// least 4 k-blocks per wave.
+// Splits so that a launch has about 256 workgroups (one per CU), each split
+// keeping at least 16 k-blocks.
 uint32_t choose_splits(uint32_t n, uint32_t k) {
-  const uint32_t groups = n % 64 == 0 ? n / 64 : n / 16;
+  const uint32_t groups = n % 64 == 0 && n < 16384 ? n / 64 : n % 32 == 0 ? n / 32 : n / 16;
   const uint32_t kb = k / 32;
-  uint32_t s = (512 + groups - 1) / groups;
+  uint32_t s = 256 / groups;
   const uint32_t max_s = kb / 16 > 0 ? kb / 16 : 1;
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;

@@ -95,116 +95,128 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* _
   if (bad) raise_error(err, ERR_NONFINITE);
 }
 
-// Per-row QK-norm over the 128-wide heads, split-half RoPE, and the paged KV
-// append, fused. One workgroup per token row:
-//  1. the row's q and k heads are staged in LDS as f32;
-//  2. thread h < heads sums its head's squares serially in ascending order,
-//     which is exactly qwen3_rmsnorm_v1 at width 128 (rmsnorm.rs:421-438, as
-//     called for QK-norm at tp_execution/batched.rs:1956-1982);
-//  3. every (head, pair) computes bf16(bf16(x*inv)*w) for both halves, then
-//     the RoPE pair with separately rounded products (rope_kv.rs:102-240,
-//     v5 rope_kv.rs:60-80): a' = a*c - b*s, b' = b*c + a*s, each narrowed once;
+// Per-head QK-norm, split-half RoPE and the paged KV append, fused. One
+// wave per (token row, head); the heads of a row are the query heads, then
+// the key heads, then the value heads of the packed QKV projection. Lane l
+// owns elements l and l + 64 of its head, which is exactly one RoPE pair.
+//  1. the projection output is bf16(P_0 + P_1 + ... + P_{S-1}) over the
+//     split-K slabs, added in split order and rounded once (the reference's
+//     one RNE per projection output), or the bf16 row itself (S = 0);
+//  2. q and k heads: the sum of squares runs serially in ascending element
+//     order (readlane chain), which is exactly qwen3_rmsnorm_v1 at width 128
+//     (rmsnorm.rs:421-438, as called for QK-norm at
+//     tp_execution/batched.rs:1956-1982);
+//  3. bf16(bf16(x*inv)*w) for both halves, then the RoPE pair with separately
+//     rounded products (rope_kv.rs:102-240, v5 rope_kv.rs:60-80):
+//     a' = a*c - b*s, b' = b*c + a*s, each narrowed once;
 //  4. rotated k and raw v go to cache[(page*16 + pos%16)][kv_head][128], the
 //     slot of qwen3_paged_kv_write_v1 (rope_kv.rs:261-388).
-__global__ __launch_bounds__(kNormThreads) void qknorm_rope_kv_kernel(
+// S < 0 takes the split count from the argument (any count); S > 0 fixes it
+// at compile time so every slab load of a lane is in flight at once.
+constexpr int kHeadsPerGroup = 4;
+
+template <int S>
+__global__ __launch_bounds__(kHeadsPerGroup * 64) void qknorm_rope_kv_kernel(
     const uint16_t* __restrict__ qkv, const float* __restrict__ qkv_part, uint32_t splits,
     const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint32_t qh,
     uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err) {
-  extern __shared__ float smem[];
-  const uint32_t heads = qh + kvh;            // heads that are normalized and rotated
-  const uint32_t all_heads = qh + 2 * kvh;    // plus the V heads
-  float* xs = smem;                           // [all_heads][129] (padded against bank conflicts)
-  float* inv_s = smem + all_heads * 129;      // [heads]
-  const uint32_t row = blockIdx.x;
-  const uint32_t ld = all_heads * 128;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t head = blockIdx.x * kHeadsPerGroup + (threadIdx.x >> 6);
+  const uint32_t row = blockIdx.y;
+  const uint32_t heads = qh + kvh;  // normalized and rotated heads
+  if (head >= heads + kvh) return;
+  const uint32_t ld = (heads + kvh) * 128;
+  const uint64_t base = (uint64_t)row * ld + head * 128 + lane;
 
-  // Projection outputs of this row, as bf16 values: either the bf16 row, or
-  // bf16(P_0 + P_1 + ...) over the split-K slabs (one rounding, as the
-  // reference's one RNE per projection output).
-  if (splits == 0) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(qkv + (uint64_t)row * ld);
-    for (uint32_t e = threadIdx.x; e < all_heads * 64; e += kNormThreads) {
-      const uint32_t word = src[e];
-      const uint32_t h = e >> 6, d = (e & 63u) * 2;
-      xs[h * 129 + d] = lo_bf16(word);
-      xs[h * 129 + d + 1] = hi_bf16(word);
-    }
+  float a, b;
+  if constexpr (S == 0) {
+    a = bf16_to_f32(qkv[base]);
+    b = bf16_to_f32(qkv[base + 64]);
   } else {
     const uint64_t slab = (uint64_t)kMaxRows * ld;
-    const float* src = qkv_part + (uint64_t)row * ld;
-    for (uint32_t e = threadIdx.x; e < all_heads * 128; e += kNormThreads) {
-      float acc = src[e];
-      for (uint32_t sp = 1; sp < splits; ++sp) acc += src[sp * slab + e];
-      xs[(e >> 7) * 129 + (e & 127u)] = round_bf16(acc);
+    if constexpr (S > 0) {
+      float pa[S], pb[S];
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp) {
+        pa[sp] = qkv_part[sp * slab + base];
+        pb[sp] = qkv_part[sp * slab + base + 64];
+      }
+      a = pa[0];
+      b = pb[0];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) {
+        a += pa[sp];
+        b += pb[sp];
+      }
+    } else {
+      a = qkv_part[base];
+      b = qkv_part[base + 64];
+      for (uint32_t sp = 1; sp < splits; ++sp) {
+        a += qkv_part[sp * slab + base];
+        b += qkv_part[sp * slab + base + 64];
+      }
     }
+    a = round_bf16(a);
+    b = round_bf16(b);
   }
-  __syncthreads();
-  if (threadIdx.x < heads) {
-    const float* xh = xs + threadIdx.x * 129;
-    float sum = 0.f;
-    bool bad = false;
-    for (int d = 0; d < 128; ++d) {
-      float a = xh[d];
-      bad |= !is_finite_f32(a);
-      float sq = a * a;
-      sum = sum + sq;
-    }
-    float inv = inverse_rms(sum, 128.0f, eps);
-    if (bad || !is_finite_f32(sum) || !is_finite_f32(inv)) raise_error(err, ERR_NONFINITE);
-    inv_s[threadIdx.x] = inv;
-  }
-  __syncthreads();
 
   const uint32_t pos = positions[row];
-  uint32_t slot_base = 0;
+  uint32_t slot = 0;
   bool slot_ok = pos < context && pos / 16 < stride;
   if (slot_ok) {
-    uint32_t page = table[(uint64_t)row * stride + pos / 16];
+    const uint32_t page = table[(uint64_t)row * stride + pos / 16];
     slot_ok = page < pages;
-    slot_base = (page * 16u + (pos & 15u)) * kvh;
+    slot = (page * 16u + (pos & 15u)) * kvh;
   }
-  if (!slot_ok) {
-    if (threadIdx.x == 0) raise_error(err, ERR_PAGE);
-  }
-  const uint32_t trig = (pos < context ? pos : 0) * 64;
-  bool bad = false;
-  for (uint32_t item = threadIdx.x; item < heads * 64; item += kNormThreads) {
-    uint32_t h = item >> 6, i = item & 63u;
-    const float* xh = xs + h * 129;
-    const uint16_t* wn = h < qh ? q_norm : k_norm;
-    float inv = inv_s[h];
-    float a = bf16_to_f32(norm_weight_bf16(xh[i], inv, bf16_to_f32(wn[i])));
-    float b = bf16_to_f32(norm_weight_bf16(xh[i + 64], inv, bf16_to_f32(wn[i + 64])));
-    float c = cos_t[trig + i], s = sin_t[trig + i];
-    float a_cos = a * c, b_sin = b * s, b_cos = b * c, a_sin = a * s;
-    uint32_t ra = f32_to_bf16(a_cos - b_sin);
-    uint32_t rb = f32_to_bf16(b_cos + a_sin);
-    bad |= ((ra & 0x7f80u) == 0x7f80u) | ((rb & 0x7f80u) == 0x7f80u);
-    if (h < qh) {
-      uint16_t* qo = q_out + (uint64_t)row * qh * 128 + h * 128;
-      qo[i] = (uint16_t)ra;
-      qo[i + 64] = (uint16_t)rb;
-    } else if (slot_ok) {
-      uint16_t* ko = k_cache + ((uint64_t)slot_base + (h - qh)) * 128;
-      ko[i] = (uint16_t)ra;
-      ko[i + 64] = (uint16_t)rb;
+  if (!slot_ok && head == 0 && lane == 0) raise_error(err, ERR_PAGE);
+
+  if (head >= heads) {
+    // Raw V (neither normalized nor rotated) into the slot.
+    if (slot_ok) {
+      uint16_t* vo = v_cache + ((uint64_t)slot + (head - heads)) * 128;
+      vo[lane] = (uint16_t)f32_to_bf16(a);
+      vo[lane + 64] = (uint16_t)f32_to_bf16(b);
     }
+    return;
   }
-  if (slot_ok) {
-    // Raw V (neither normalized nor rotated) into the same slot.
-    uint32_t* vdst = reinterpret_cast<uint32_t*>(v_cache + (uint64_t)slot_base * 128);
-    for (uint32_t e = threadIdx.x; e < kvh * 64; e += kNormThreads) {
-      const float* xv = xs + (heads + (e >> 6)) * 129 + (e & 63u) * 2;
-      vdst[e] = f32_to_bf16(xv[0]) | (f32_to_bf16(xv[1]) << 16);
-    }
+
+  bool bad = !is_finite_f32(a) | !is_finite_f32(b);
+  const float sqa = a * a, sqb = b * b;
+  float sum = 0.f;
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqa, l);
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqb, l);
+  const float inv = inverse_rms(sum, 128.0f, eps);
+  bad |= !is_finite_f32(sum) | !is_finite_f32(inv);
+
+  const uint16_t* wn = head < qh ? q_norm : k_norm;
+  const float an = bf16_to_f32(norm_weight_bf16(a, inv, bf16_to_f32(wn[lane])));
+  const float bn = bf16_to_f32(norm_weight_bf16(b, inv, bf16_to_f32(wn[lane + 64])));
+  const uint32_t trig = (pos < context ? pos : 0) * 64 + lane;
+  const float c = cos_t[trig], s = sin_t[trig];
+  const float a_cos = an * c, b_sin = bn * s, b_cos = bn * c, a_sin = an * s;
+  const uint32_t ra = f32_to_bf16(a_cos - b_sin);
+  const uint32_t rb = f32_to_bf16(b_cos + a_sin);
+  bad |= ((ra & 0x7f80u) == 0x7f80u) | ((rb & 0x7f80u) == 0x7f80u);
+  uint16_t* dst = nullptr;
+  if (head < qh)
+    dst = q_out + ((uint64_t)row * qh + head) * 128;
+  else if (slot_ok)
+    dst = k_cache + ((uint64_t)slot + (head - qh)) * 128;
+  if (dst) {
+    dst[lane] = (uint16_t)ra;
+    dst[lane + 64] = (uint16_t)rb;
   }
   if (bad) raise_error(err, ERR_NONFINITE);
 }
 
 // Residual + RMSNorm (see fh_op_residual_rmsnorm): one workgroup per row,
-// 16-byte chunks c = tid, tid + 256, ... of the row.
+// 16-byte chunks c = tid, tid + 256, ... of the row. S as in the QK-norm
+// kernel: 0 = no partials, > 0 = compile-time split count, < 0 = any count.
+template <int S>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t* __restrict__ hidden,
                                                                         const float* __restrict__ part,
                                                                         uint32_t splits,
@@ -225,16 +237,34 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
     const uint32_t c = threadIdx.x + j * kNormThreads;
     if (c < chunks) {
       v[j] = *reinterpret_cast<const uint4*>(hr + c * 8);
-      if (splits) {
+      if constexpr (S != 0) {
         // h = bf16((0 + (P_0 + P_1 + ...)) + h), v5 collective.rs:25-60 with
         // the split-K slabs added in split order.
-        const float* pr = part + (uint64_t)row * width + c * 8;
+        const float4* pr = reinterpret_cast<const float4*>(part + (uint64_t)row * width + c * 8);
+        const uint64_t slab4 = slab / 4;
         float a[8];
+        if constexpr (S > 0) {
+          float4 p[S][2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = pr[e];
-        for (uint32_t sp = 1; sp < splits; ++sp)
+          for (int sp = 0; sp < S; ++sp) {
+            p[sp][0] = pr[sp * slab4];
+            p[sp][1] = pr[sp * slab4 + 1];
+          }
+          a[0] = p[0][0].x; a[1] = p[0][0].y; a[2] = p[0][0].z; a[3] = p[0][0].w;
+          a[4] = p[0][1].x; a[5] = p[0][1].y; a[6] = p[0][1].z; a[7] = p[0][1].w;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] += pr[sp * slab + e];
+          for (int sp = 1; sp < S; ++sp) {
+            a[0] += p[sp][0].x; a[1] += p[sp][0].y; a[2] += p[sp][0].z; a[3] += p[sp][0].w;
+            a[4] += p[sp][1].x; a[5] += p[sp][1].y; a[6] += p[sp][1].z; a[7] += p[sp][1].w;
+          }
+        } else {
+          const float* pf = reinterpret_cast<const float*>(pr);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] = pf[e];
+          for (uint32_t sp = 1; sp < splits; ++sp)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] += pf[sp * slab + e];
+        }
         uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -322,18 +352,42 @@ hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uin
                                  uint16_t* k_cache, uint16_t* v_cache, uint32_t rows, uint32_t qh, uint32_t kvh,
                                  uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err,
                                  hipStream_t s) {
-  size_t lds = ((size_t)(qh + 2 * kvh) * 129 + (qh + kvh)) * sizeof(float);
-  hipLaunchKernelGGL(qknorm_rope_kv_kernel, dim3(rows), dim3(kNormThreads), lds, s, qkv, qkv_part, splits, q_norm,
-                     k_norm, cos_t, sin_t, positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context,
-                     eps, err);
+  const dim3 grid((qh + 2 * kvh + kHeadsPerGroup - 1) / kHeadsPerGroup, rows);
+  const dim3 block(kHeadsPerGroup * 64);
+#define FH_QKNORM(S_)                                                                                              \
+  hipLaunchKernelGGL(qknorm_rope_kv_kernel<S_>, grid, block, 0, s, qkv, qkv_part, splits, q_norm, k_norm, cos_t,  \
+                     sin_t, positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context, eps, err)
+  switch (qkv_part ? splits : 0) {
+    case 0: FH_QKNORM(0); break;
+    case 1: FH_QKNORM(1); break;
+    case 2: FH_QKNORM(2); break;
+    case 3: FH_QKNORM(3); break;
+    case 4: FH_QKNORM(4); break;
+    case 6: FH_QKNORM(6); break;
+    case 8: FH_QKNORM(8); break;
+    default: FH_QKNORM(-1); break;
+  }
+#undef FH_QKNORM
   return hipGetLastError();
 }
 
 hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* w,
                                    uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float eps,
                                    uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, y,
-                     y_tiled, width, eps, err);
+#define FH_RESNORM(S_)                                                                                             \
+  hipLaunchKernelGGL(residual_rmsnorm_kernel<S_>, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, \
+                     y, y_tiled, width, eps, err)
+  switch (partials ? splits : 0) {
+    case 0: FH_RESNORM(0); break;
+    case 1: FH_RESNORM(1); break;
+    case 2: FH_RESNORM(2); break;
+    case 3: FH_RESNORM(3); break;
+    case 4: FH_RESNORM(4); break;
+    case 6: FH_RESNORM(6); break;
+    case 8: FH_RESNORM(8); break;
+    default: FH_RESNORM(-1); break;
+  }
+#undef FH_RESNORM
   return hipGetLastError();
 }
 

@@ -7,6 +7,9 @@
 
 namespace fh {
 
+// Records the message fh_last_error(NULL) returns on this thread.
+void set_thread_error(const char* msg);
+
 // Attention partition: each partition workgroup covers this many pages of
 // 16 tokens (8 per wave).
 constexpr uint32_t kAttnSplitPages = 32;

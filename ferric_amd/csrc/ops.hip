@@ -11,7 +11,16 @@ namespace {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline fh_status from_hip(hipError_t e) { return e == hipSuccess ? FH_OK : FH_ERR_DEVICE; }
+inline fh_status status_of(hipError_t e) {
+  if (e == hipSuccess) return FH_OK;
+  fh::set_thread_error(hipGetErrorString(e));
+  return FH_ERR_DEVICE;
+}
+
+// Launchers report hipGetLastError(), which also returns an error left
+// behind by an unrelated earlier runtime call on this thread; clear it first
+// so that the status belongs to this launch.
+#define from_hip(expr) (static_cast<void>(hipGetLastError()), status_of(expr))
 
 }  // namespace
 
@@ -25,9 +34,10 @@ fh_status fh_op_tile_weight(const uint16_t* src, uint16_t* dst, uint32_t n, uint
 fh_status fh_op_tile_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* dst, uint32_t i, uint32_t k,
                              void* stream) {
   if (!gate || !up || !dst || i == 0 || k == 0 || i % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  (void)hipGetLastError();
   hipError_t e = fh::launch_tile_weight(gate, dst, i, k, 2, 0, as_stream(stream));
   if (e == hipSuccess) e = fh::launch_tile_weight(up, dst, i, k, 2, 1, as_stream(stream));
-  return from_hip(e);
+  return status_of(e);
 }
 
 fh_status fh_op_untile_weight(const uint16_t* tiled, uint16_t* dst, uint32_t n, uint32_t k, void* stream) {

@@ -343,6 +343,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   const uint32_t* d_tab = ctx->d_meta + 2 * cap;
   uint32_t* err = ctx->err;
   Enq q{ctx};
+  (void)hipGetLastError();  // launch statuses below then belong to these launches
   uint64_t n = 0;
   auto L = [&](uint32_t cls, auto&& f) {
     q.run(cls, f);
@@ -429,6 +430,11 @@ std::string error_bits(uint32_t e) {
 }
 
 }  // namespace
+
+namespace fh {
+// Message for fh_last_error(NULL) after a failed context-free call.
+void set_thread_error(const char* msg) { g_create_error = msg; }
+}  // namespace fh
 
 extern "C" {
 

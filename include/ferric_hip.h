@@ -113,7 +113,8 @@ typedef struct fh_ctx fh_ctx;
 fh_status fh_create(const fh_model_desc* model, const fh_ctx_options* options, fh_ctx** out);
 /* Releases every device allocation (replaces close(), tp_batch_runtime.rs:93). */
 void fh_destroy(fh_ctx* ctx);
-/* Message of the last failure on this context, or of the last failed fh_create when ctx is NULL. */
+/* Message of the last failure on this context, or, when ctx is NULL, of the
+   last failed fh_create or fh_op_* launch on the calling thread. */
 const char* fh_last_error(const fh_ctx* ctx);
 
 /* Uploads one row-major bf16 weight [N][K] (nn.Linear layout; norms are [width]).

@@ -81,10 +81,13 @@ def test_scratch_sizes():
     # 32 rows x 32 heads x ceil(8320 / 512) partitions x (2 + 128) f32
     assert lib.fh_attention_scratch_bytes(32, 32, 8320) == 32 * 32 * 17 * 130 * 4
     assert lib.fh_argmax_scratch_bytes(32) == 32 * 64 * 8
-    # split-K factors keep about 512 workgroups per projection launch
-    assert lib.fh_gemm_default_splits(6144, 4096) >= 4
-    assert lib.fh_gemm_default_splits(24576, 4096) == 2
-    assert lib.fh_gemm_default_splits(151936, 4096) == 1
+    # split-K factors keep about 256 workgroups per projection launch
+    assert lib.fh_gemm_default_splits(4096, 4096) == 4  # o
+    assert lib.fh_gemm_default_splits(6144, 4096) == 2  # packed qkv
+    assert lib.fh_gemm_default_splits(4096, 12288) == 4  # down
+    assert lib.fh_gemm_default_splits(24576, 4096) == 1  # gate/up
+    assert lib.fh_gemm_default_splits(151936, 4096) == 1  # LM head
+    assert lib.fh_gemm_default_splits(1024, 2048) == 4  # capped at 16 k-blocks per split
 
 
 def test_ops_reject_bad_shapes_before_any_launch():
@@ -139,3 +142,17 @@ def test_page_pool_reserves_write_slots_and_consecutive_positions():
     assert len(all_pages) == len(set(all_pages))
     with pytest.raises(ValueError):
         pool.prepare([(a, 1)] * 120)
+
+
+def test_library_shares_torch_hip_runtime():
+    # Importing the package before torch must still leave one HIP runtime in
+    # the process (two copies disagree about which devices exist).
+    import subprocess
+    import sys
+
+    code = ("import ferric_amd, torch\n"
+            "maps = open('/proc/self/maps').read().splitlines()\n"
+            "print(len({l.split()[-1] for l in maps if 'libamdhip64' in l}))\n")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "1"
