@@ -8,11 +8,12 @@ sequence context lengths uniform in [512, 8192] (seeded) of random KV
 greedy decode. A step is one fh_execute_batch over the 32 rows: tokens in,
 greedy choices out, KV appended; the chosen tokens feed the next step.
 
-Prints one JSON line (see the contract in the repository's build notes):
-value = whole-job decode tokens/s; roofline = the dominant kernel's
-algorithmic HBM bytes per launch / its average launch time (HIP events on
-the runner's stream, recorded around every launch of the timed steps);
-cpu_baseline = the CPU oracle timed on a bounded sample of the same step.
+Prints one JSON line: value = whole-job decode tokens/s over the timed steps
+(HIP graph replays, as served; --eager times plain launches instead);
+roofline = the dominant kernel's algorithmic HBM bytes per launch / its
+average launch time, from HIP events recorded on the runner's stream around
+every launch of --profile-steps further eager steps; cpu_baseline = the CPU
+oracle timed on a bounded sample of the same step.
 """
 
 from __future__ import annotations
@@ -52,10 +53,27 @@ def parse():
     p.add_argument("--workload", default="qwen3-8b-b32", choices=sorted(WORKLOADS))
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-layers", type=int, default=2, help="layers the CPU oracle sample runs")
-    p.add_argument("--graphs", action="store_true",
-                   help="replay HIP graphs in the timed region (no per-launch events)")
+    p.add_argument("--cpu-steps", type=int, default=2, help="decode steps the CPU oracle sample runs")
+    p.add_argument("--eager", action="store_true", help="time eager launches instead of HIP graph replays")
+    p.add_argument("--profile-steps", type=int, default=16,
+                   help="eager steps with per-launch HIP events after the timed steps (per-kernel times, roofline)")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="only run 4 device-to-device copies of this many MiB (calibrates HBM byte counters) and exit")
     return p.parse_args()
+
+
+def copy_probe(mib):
+    """Four plain copies of a known size: under a hardware-counter profiler
+    their FETCH_SIZE / WRITE_SIZE per dispatch give the counters' scale."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 4}), flush=True)
 
 
 def kernel_bytes(cfg, rows, positions, stride):
@@ -95,42 +113,44 @@ def step_bytes(cfg, rows, positions):
 
 
 def cpu_baseline(cfg, contexts, args, seed):
-    """Times the CPU oracle on one decode step of the same workload restricted
-    to the first args.cpu_layers layers (+ embedding, final norm, FP32 head,
-    argmax), then extrapolates to the full depth."""
+    """Times the CPU oracle (all layers, same weights-generator, contexts and
+    KV shapes) on args.cpu_steps consecutive decode steps of the workload."""
     from oracle import oracle as orc
 
-    sample_cfg = dict(cfg, layers=args.cpu_layers)
     rows = len(contexts)
-    stride = (max(contexts) + 1 + 15) // 16 + 1
-    pages = sum((c + 1 + 15) // 16 for c in contexts) + rows
-    m = orc.Model(sample_cfg, pages)
+    steps = args.cpu_steps
+    need = [(c + steps + 15) // 16 for c in contexts]
+    stride = max(need) + 1
+    pages = sum(need) + rows
+    m = orc.Model(cfg, pages)
     try:
         t0 = time.perf_counter()
         m.synthesize(seed, 0.02)
         tables = np.full((rows, stride), 0xFFFFFFFF, np.uint32)
-        counts = np.zeros(rows, np.uint32)
         nxt = 0
-        for i, c in enumerate(contexts):
-            n = (c + 1 + 15) // 16
+        for i, n in enumerate(need):
             tables[i, :n] = np.arange(nxt, nxt + n, dtype=np.uint32)
-            counts[i] = n
             nxt += n
         m.kv_fill(seed, 1.0, tables, stride, contexts, list(range(1, rows + 1)), 1 << 20)
         setup_s = time.perf_counter() - t0
         toks = np.random.default_rng(seed).integers(0, cfg["vocabulary"], rows)
-        out = m.forward(toks, contexts, tables, counts, stride, want_logits=False)
-        per_layer = out["seconds_layers"] / args.cpu_layers
-        step_s = per_layer * cfg["layers"] + out["seconds_rest"]
+        positions = np.asarray(contexts, np.int64)
+        elapsed = 0.0
+        for _ in range(steps):
+            counts = np.asarray([(p + 1 + 15) // 16 for p in positions], np.uint32)
+            t1 = time.perf_counter()
+            out = m.forward(toks, positions, tables, counts, stride, want_logits=False)
+            elapsed += time.perf_counter() - t1
+            toks = out["choices"]
+            positions = positions + 1
         return {
-            "value": rows / step_s,
+            "value": rows * steps / elapsed,
             "unit": "tokens/s",
             "cores": orc.threads(),
             "kind": "port",
-            "sample": (f"1 decode step, batch {rows}, same contexts; first {args.cpu_layers} of {cfg['layers']} layers "
-                       f"({out['seconds_layers']:.2f} s) + embedding/final norm/FP32 head/argmax "
-                       f"({out['seconds_rest']:.2f} s); per-layer time x {cfg['layers']} => {step_s:.2f} s/step "
-                       f"(setup {setup_s:.1f} s untimed)"),
+            "sample": (f"{steps} full decode steps ({cfg['layers']} layers, embedding, final norm, FP32 head, "
+                       f"argmax) at batch {rows} over the same contexts: {elapsed:.2f} s "
+                       f"(weights + KV prefix generation {setup_s:.1f} s untimed)"),
         }
     finally:
         m.close()
@@ -142,6 +162,9 @@ def main():
         print(f"bench.py measures one GPU: every box in this build has one MI355X, so --gpus {args.gpus} is not "
               f"supported (the batch shards by sequence across GPUs; see the sharding notes)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
 
     import torch
 
@@ -151,7 +174,7 @@ def main():
     name = args.workload
     model_key, batch, (ctx_lo, ctx_hi), phys_pages, headroom, desc = WORKLOADS[name]
     cfg = dict(ferric_amd.QWEN3_8B if model_key == "8b" else ferric_amd.QWEN3_0_6B)
-    context_tokens = ctx_hi + headroom + args.warmup + args.steps
+    context_tokens = ctx_hi + headroom + args.warmup + args.steps + args.profile_steps
     context_tokens = (context_tokens + 15) // 16 * 16
     limits = PagedLimits(context_tokens=context_tokens, physical_page_count=phys_pages,
                          page_table_stride=context_tokens // 16)
@@ -159,7 +182,7 @@ def main():
     contexts = [int(c) for c in rng.integers(ctx_lo, ctx_hi + 1, batch)]
 
     t_setup = time.perf_counter()
-    runner = TpBatchRunner(cfg, limits, row_capacity=32, use_graphs=args.graphs)
+    runner = TpBatchRunner(cfg, limits, row_capacity=32, use_graphs=not args.eager)
     runner.synthesize_weights(args.seed, 0.02)
     pool = PagePool(limits, seed=args.seed)
     sids = [pool.admit(c) for c in contexts]
@@ -179,28 +202,28 @@ def main():
     for _ in range(args.warmup):
         tokens, _ = step(tokens)
 
-    profile = not args.graphs
-    runner.set_profiling(profile)
-    class_ms = {}
-    class_launches = {}
-    class_bytes = {}
     step_byte_total = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tokens, positions = step(tokens)
-        if profile:
-            for k, (ms, n) in runner.kernel_class_ms().items():
-                class_ms[k] = class_ms.get(k, 0.0) + ms
-                class_launches[k] = class_launches.get(k, 0) + n
-            for k, b in kernel_bytes(cfg, batch, positions, limits.page_table_stride).items():
-                per_layer = cfg["layers"] if k not in ("head_gemm", "argmax", "embedding") else 1
-                if k == "rmsnorm":
-                    per_layer = 2 * cfg["layers"] + 1
-                class_bytes[k] = class_bytes.get(k, 0) + b * per_layer
         step_byte_total += step_bytes(cfg, batch, positions)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+
+    # Per-kernel times: eager steps with an event pair around every launch.
+    class_ms, class_launches, class_bytes = {}, {}, {}
+    runner.set_profiling(args.profile_steps > 0)
+    for _ in range(args.profile_steps):
+        tokens, positions = step(tokens)
+        for k, (ms, n) in runner.kernel_class_ms().items():
+            class_ms[k] = class_ms.get(k, 0.0) + ms
+            class_launches[k] = class_launches.get(k, 0) + n
+        for k, b in kernel_bytes(cfg, batch, positions, limits.page_table_stride).items():
+            per_layer = cfg["layers"] if k not in ("head_gemm", "argmax", "embedding") else 1
+            if k == "rmsnorm":
+                per_layer = 2 * cfg["layers"] + 1
+            class_bytes[k] = class_bytes.get(k, 0) + b * per_layer
     runner.set_profiling(False)
 
     ms_per_step = elapsed * 1e3 / args.steps
@@ -222,12 +245,12 @@ def main():
         "data": "synthetic (device-generated weights ~N(0,0.02), random KV prefixes ~N(0,1), seeded)",
         "config": {"workload": desc, "batch": batch, "contexts_mean": round(float(np.mean(contexts)), 1),
                    "decode_steps_timed": args.steps, "page_tokens": 16, "physical_pages": phys_pages,
-                   "graphs": bool(args.graphs)},
+                   "graphs": not args.eager, "profile_steps": args.profile_steps},
         "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(step_gbs / PEAK_HBM_GBS, 4),
                      "bytes_per_step": int(step_byte_total / args.steps)},
     }
-    if profile and class_ms:
+    if class_ms:
         dominant = max(class_ms, key=lambda k: class_ms[k])
         avg_ms = class_ms[dominant] / max(class_launches[dominant], 1)
         bytes_per_launch = class_bytes.get(dominant, 0) / max(class_launches[dominant], 1)
@@ -237,7 +260,7 @@ def main():
                               "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 2),
                               "algorithmic_bytes_per_launch": int(bytes_per_launch)}
         result["kernels"] = {
-            k: {"ms_per_step": round(class_ms[k] / args.steps, 4),
+            k: {"ms_per_step": round(class_ms[k] / args.profile_steps, 4),
                 "gbs": round(class_bytes.get(k, 0) / (class_ms[k] * 1e-3) / 1e9, 1) if class_ms[k] > 0 else None}
             for k in sorted(class_ms, key=lambda k: -class_ms[k])}
     if not args.no_cpu_baseline:
