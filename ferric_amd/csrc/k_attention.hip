@@ -7,27 +7,28 @@
 // reference's split variant (device/qwen3-tp-c1-split8-attention-kernels-v21,
 // README.md:42-80) partitions the context, keeps an FP32 state (m, l, n[128])
 // per partition, merges the partitions in ascending order, then divides and
-// narrows once. This kernel pair keeps that contract with 32-page (512-token)
-// partitions and GQA sharing: one workgroup serves the G query heads of one KV
-// head, so every K/V page is read from HBM once per token row.
+// narrows once. This kernel pair keeps that contract with kAttnSplitPages-page
+// partitions.
 //
-// Partition kernel, grid (partition, kv_head, row), 4 waves; wave w walks 8
-// consecutive pages of the partition, one page (16 tokens) per iteration,
-// with the next page's K and V loads in flight while the current page is
-// computed:
-//   QK^T on MFMA: S^T = K Q^T, the 16-token K page as the A operand straight
-//   from the paged cache (lane l holds token l % 16; MFMA i covers dims
-//   32 i .. 32 i + 31, so each load instruction reads 64 contiguous bytes of
-//   every token), the G queries as the B operand (registers).
-//   Online softmax per page (page max, rescale, exp, page sum).
-//   PV on VALU: lane l owns output dims 2l, 2l+1; a token's V row is one
-//   coalesced 256-byte wave load.
-// The four wave states are merged in wave order. A row whose context fits
-// one partition is finished here (divide, narrow, store); longer rows leave
-// partition states for the merge kernel.
+// Partition kernel, grid (partition, KV head, row), 4 waves; each wave takes
+// 4 of the partition's 16 pages and the G query heads of the KV head, so
+// every K/V byte is read once per token row. A wave makes two memory round
+// trips, each with all of its pages' loads in flight at once:
+//   1. K: whole 256-byte token rows per load, re-laid through a padded LDS
+//      tile into the MFMA A operand (lane l: token l % 16, dims 32 i + 8 (l/16)
+//      for MFMA i); S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the G queries
+//      as the B operand; scaled, masked scores go to LDS.
+//   2. Exact softmax over the wave's 64 tokens (max, p = exp(s - max), sum),
+//      then PV on VALU: lane l owns output dims 2l, 2l+1, and a token's V row
+//      is one coalesced 256-byte wave load.
+// The four wave states (m, l, n[128]) are merged in wave order. A row whose
+// context fits one partition is finished here (divide, narrow, store);
+// longer rows leave partition states for the merge kernel.
 // Merge kernel: one wave per (row, query head). Partition weights
 // w_p = exp(m_p - M) with M the maximum over partitions, then l and n are
 // summed over partitions in ascending order, divided, narrowed once.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -36,10 +37,17 @@ namespace fh {
 namespace {
 
 constexpr int kAttnThreads = 256;
-constexpr uint32_t kWavePages = kAttnSplitPages / 4;
 constexpr uint32_t kScaleBits = 0x3db504f3u;  // f32 1/sqrt(128), paged_decode.rs:31-35
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32, about 1 ulp). The
+// reference uses the library expf; the softmax terms it feeds are compared
+// to tolerance, and the relative difference here is below 1e-6 for the
+// |x| < 100 that a max-subtracted softmax sees. exp(-inf) = 0 as required.
+__device__ __forceinline__ float exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
 
 // Stores one finished head output (dims 2*lane, 2*lane+1) in either layout.
 __device__ __forceinline__ void store_head(uint16_t* out, bool tiled, uint32_t r, uint32_t qh, uint32_t head, int lane,
@@ -52,13 +60,21 @@ __device__ __forceinline__ void store_head(uint16_t* out, bool tiled, uint32_t r
     reinterpret_cast<uint32_t*>(out + ((uint64_t)r * qh + head) * 128)[lane] = word;
 }
 
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_partition_kernel(
+// One workgroup per (partition, KV head, row); its WAVES waves split the
+// partition's pages (kAttnSplitPages / WAVES each) and serve the G query
+// heads of the KV head. A wave issues all of its K loads at once, scores them,
+// then issues all of its V loads at once: two memory round trips per wave.
+template <int G, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, float* __restrict__ part,
     uint16_t* __restrict__ out, uint32_t out_tiled, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
     uint32_t context, uint32_t smax, uint32_t* err) {
+  constexpr uint32_t kWavePages = kAttnSplitPages / WAVES;
+  static_assert(kAttnSplitPages % WAVES == 0, "pages split evenly over the waves");
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
+  // The wave index is uniform; saying so keeps every page address scalar.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t pos = positions[r];
   if (pos >= context || pos / 16 >= stride) {
     if (split == 0 && h == 0 && threadIdx.x == 0) raise_error(err, ERR_POSITION);
@@ -69,16 +85,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partition_kernel(
   const uint32_t p0 = split * kAttnSplitPages;
   if (p0 >= row_pages) return;  // uniform per workgroup
   const uint32_t nsplit = (row_pages + kAttnSplitPages - 1) / kAttnSplitPages;
+  // This wave's pages: [w0, w0 + np) of the row.
+  const uint32_t w0 = p0 + wave * kWavePages;
+  const uint32_t np = w0 < row_pages ? min(row_pages - w0, kWavePages) : 0u;
 
-  __shared__ float pbuf[4][16][G];
-  __shared__ float wstat[4][2][G];
-  __shared__ float wacc[4][G][128];
+  // Scores of the wave's tokens, replaced in place by probabilities: [token][g].
+  __shared__ float sbuf[WAVES][kWavePages * 16][G];
+  __shared__ float wstat[WAVES][2][G];
+  __shared__ float wacc[WAVES][G][128];
+  float* sw = &sbuf[wave][0][0];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g16 = lane >> 4, r16 = lane & 15;
   const float scale = __builtin_bit_cast(float, kScaleBits);
   const float kNegInf = -__builtin_inff();
   const uint32_t* trow = table + (uint64_t)r * stride;
+  bool bad = false;
 
   // B operand: query head h*G + r16 (zero for r16 >= G); MFMA i, lane group
   // g16 covers dims 32*i + 8*g16 .. +7.
@@ -92,113 +113,148 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partition_kernel(
     for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  const uint32_t wp0 = p0 + wave * kWavePages;
-  const uint32_t wp1 = min(min(wp0 + kWavePages, p0 + kAttnSplitPages), row_pages);
-  const int np = wp1 > wp0 ? (int)(wp1 - wp0) : 0;
-  const uint32_t vstride = kvh * 64;  // dwords between consecutive slots of one head
-
-  float m[G], l[G], acc[G][2];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegInf;
-    l[g] = 0.f;
-    acc[g][0] = acc[g][1] = 0.f;
+  // Physical pages of this wave, one per lane, read back with readlane so no
+  // scalar table load sits between page loads.
+  static_assert(kWavePages <= 64, "one page-table entry per lane");
+  uint32_t my_phys = lane < (int)np ? trow[w0 + lane] : 0u;
+  if (my_phys >= pages) {
+    bad = true;
+    my_phys = 0;
   }
-  bool bad = false;
+  auto phys_of = [&](uint32_t j) { return (uint32_t)__builtin_amdgcn_readlane((int)my_phys, (int)j); };
 
-  u32x4 kcur[4], knext[4];
-  uint32_t vcur[16], vnext[16];
-  auto load_page = [&](uint32_t page, u32x4* kd, uint32_t* vd) {
-    uint32_t phys = trow[page];
-    if (phys >= pages) {
-      bad = true;
-      phys = 0;
-    }
-    const uint16_t* kp = kc + (((uint64_t)phys * 16 + r16) * kvh + h) * 128 + 8 * g16;
+  // Pass 1: S^T = K Q^T on MFMA per page, scaled and masked scores to LDS,
+  // and each query head's maximum over the wave's tokens.
+  const uint32_t vstride = kvh * 64;  // dwords between consecutive slots of one head
+  uint32_t vd[kWavePages][16];
+  auto load_v = [&] {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kd[i] = *reinterpret_cast<const u32x4*>(kp + 32 * i);
-    const uint32_t* vp = reinterpret_cast<const uint32_t*>(vc + (((uint64_t)phys * 16) * kvh + h) * 128) + lane;
+    for (uint32_t u = 0; u < kWavePages; ++u) {
+      if (u < np) {
+        const uint32_t* vp =
+            reinterpret_cast<const uint32_t*>(vc + (((uint64_t)phys_of(u) * 16) * kvh + h) * 128) + lane;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) vd[e] = vp[e * vstride];
-  };
-
-  if (np > 0) load_page(wp0, kcur, vcur);
-  for (int j = 0; j < np; ++j) {
-    const uint32_t page = wp0 + j;
-    if (j + 1 < np) load_page(page + 1, knext, vnext);
-
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kcur[i]),
-                                                 __builtin_bit_cast(bf16x8, qv[i]), s, 0, 0, 0);
-    // Lane holds query r16 for tokens 4*g16 + e of this page.
-    const uint32_t t0 = page * 16;
-    float sc[4];
-    float pm = kNegInf;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool valid = t0 + 4 * g16 + e < ctx;
-      sc[e] = valid ? s[e] * scale : kNegInf;
-      bad |= valid && !is_finite_f32(sc[e]);
-      pm = fmaxf(pm, sc[e]);
-    }
-    pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
-    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
-    // New running max per head (wave-uniform) and the rescale factors.
-    float mnew[G], alpha[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      mnew[g] = fmaxf(m[g], lane_bcast(pm, g));
-      alpha[g] = expf(m[g] - mnew[g]);  // m = -inf on the first page: alpha = 0
-    }
-    float mine = mnew[0];
-#pragma unroll
-    for (int g = 1; g < G; ++g) mine = r16 == g ? mnew[g] : mine;
-    float ps = 0.f;
-    float pr[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pr[e] = sc[e] > kNegInf ? expf(sc[e] - mine) : 0.f;
-      ps += pr[e];
-    }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    if (r16 < G) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pbuf[wave][4 * g16 + e][r16] = pr[e];
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      l[g] = l[g] * alpha[g] + lane_bcast(ps, g);
-      acc[g][0] *= alpha[g];
-      acc[g][1] *= alpha[g];
-      m[g] = mnew[g];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t valid_tokens = min(16u, ctx - t0);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t v = (uint32_t)e < valid_tokens ? vcur[e] : 0u;
-      const float v0 = lo_bf16(v), v1 = hi_bf16(v);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = pbuf[wave][e][g];
-        acc[g][0] = fmaf(p, v0, acc[g][0]);
-        acc[g][1] = fmaf(p, v1, acc[g][1]);
+        for (int e = 0; e < 16; ++e) vd[u][e] = vp[e * vstride];
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  float pm = kNegInf;  // this lane's max for query column r16
+  auto score_page = [&](uint32_t u, const u32x4 (&ka)[4]) {
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kcur[i] = knext[i];
+    for (int i = 0; i < 4; ++i)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[i]),
+                                                    __builtin_bit_cast(bf16x8, qv[i]), sacc, 0, 0, 0);
+    // Lane holds query r16 for tokens 4*g16 + e of the page.
+    const uint32_t t = u * 16 + 4 * g16;  // token within the wave's range
 #pragma unroll
-    for (int e = 0; e < 16; ++e) vcur[e] = vnext[e];
+    for (int e = 0; e < 4; ++e) {
+      const bool valid = w0 * 16 + t + e < ctx;
+      const float sv = valid ? sacc[e] * scale : kNegInf;
+      bad |= valid && !is_finite_f32(sv);
+      pm = fmaxf(pm, sv);
+      if (r16 < G) sw[(t + e) * G + r16] = sv;
+    }
+  };
+  {
+    // Whole 256-byte token rows per load (lane: token 4 i + g16, dims
+    // 8 r16 .. 8 r16 + 7), turned into the A-operand layout through a padded
+    // LDS tile (272-byte rows keep the column reads conflict-free).
+    __shared__ u32x4 ktile[WAVES][16][17];
+    u32x4 kr[kWavePages][4];
+#pragma unroll
+    for (uint32_t u = 0; u < kWavePages; ++u) {
+      if (u < np) {
+        const uint16_t* kp = kc + (((uint64_t)phys_of(u) * 16 + g16) * kvh + h) * 128 + 8 * r16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          kr[u][i] = *reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128);
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kWavePages; ++u) {
+      if (u < np) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ktile[wave][4 * i + g16][r16] = kr[u][i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        u32x4 ka[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ka[i] = ktile[wave][r16][g16 + 4 * i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        score_page(u, ka);
+      }
+    }
+  }
+  pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
+  pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+  float m[G], l[G], acc[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) m[g] = lane_bcast(pm, g);  // lanes with r16 = g hold head g's max
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // Probabilities p = exp(s - m) in place and the denominators l (per-lane
+  // partial sums in ascending token order, then a fixed butterfly).
+  const uint32_t ntok = np * 16;
+  float ls[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) ls[g] = 0.f;
+  for (uint32_t t = lane; t < ntok; t += 64) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sv = sw[t * G + g];
+      const float pv = sv > kNegInf ? exp_fast(sv - m[g]) : 0.f;
+      sw[t * G + g] = pv;
+      ls[g] += pv;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] = wave_sum(ls[g]);
+    acc[g][0] = acc[g][1] = 0.f;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // Pass 2: n += p * v on VALU; lane l owns output dims 2l, 2l+1, and a
+  // token's V row is one coalesced 256-byte wave load.
+  {
+    load_v();
+    auto pv_page = [&](auto full_tag, uint32_t u) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      const uint32_t valid = FULL ? 16u : min(16u, ctx - (w0 + u) * 16);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t v = FULL || (uint32_t)e < valid ? vd[u][e] : 0u;  // slots past the context may hold anything
+        const float v0 = lo_bf16(v), v1 = hi_bf16(v);
+        const float* pt = sw + (u * 16 + e) * G;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pg = pt[g];
+          acc[g][0] = fmaf(pg, v0, acc[g][0]);
+          acc[g][1] = fmaf(pg, v1, acc[g][1]);
+        }
+      }
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < kWavePages; ++u) {
+      if (u < np) {
+        if ((w0 + u + 1) * 16 <= ctx)
+          pv_page(std::true_type{}, u);
+        else
+          pv_page(std::false_type{}, u);
+      }
+    }
   }
 
+  // Merge the waves' states in wave order (waves past the context have l = 0).
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -215,16 +271,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partition_kernel(
 
   if (nsplit == 1) {
     // Whole context in this partition: merge the waves, divide, narrow, store.
-    for (int g = wave; g < G; g += 4) {
+    for (int g = wave; g < G; g += WAVES) {
       float M = wstat[0][0][g];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) M = fmaxf(M, wstat[w][0][g]);
+      for (int w = 1; w < WAVES; ++w) M = fmaxf(M, wstat[w][0][g]);
       float L = 0.f, n0 = 0.f, n1 = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < WAVES; ++w) {
         const float lw = wstat[w][1][g];
         if (lw > 0.f) {
-          const float f = expf(wstat[w][0][g] - M);
+          const float f = exp_fast(wstat[w][0][g] - M);
           L += lw * f;
           n0 += wacc[w][g][2 * lane] * f;
           n1 += wacc[w][g][2 * lane + 1] * f;
@@ -235,20 +291,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partition_kernel(
       store_head(out, out_tiled != 0, r, qh, h * G + g, lane, o0, o1);
     }
   } else {
-    for (int idx = threadIdx.x; idx < G * (int)kAttnPartialFloats; idx += kAttnThreads) {
+    // Partition state (m, l, n[128]) of each query head.
+    for (int idx = threadIdx.x; idx < G * (int)kAttnPartialFloats; idx += WAVES * 64) {
       const int g = idx / (int)kAttnPartialFloats, c = idx % (int)kAttnPartialFloats;
       float M = wstat[0][0][g];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) M = fmaxf(M, wstat[w][0][g]);
+      for (int w = 1; w < WAVES; ++w) M = fmaxf(M, wstat[w][0][g]);
       float v;
       if (c == 0) {
         v = M;
       } else {
         v = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < WAVES; ++w) {
           const float lw = wstat[w][1][g];
-          if (lw > 0.f) v += (c == 1 ? lw : wacc[w][g][c - 2]) * expf(wstat[w][0][g] - M);
+          if (lw > 0.f) v += (c == 1 ? lw : wacc[w][g][c - 2]) * exp_fast(wstat[w][0][g] - M);
         }
       }
       part[(((uint64_t)r * qh + h * G + g) * smax + split) * kAttnPartialFloats + c] = v;
@@ -272,30 +329,37 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
   const uint32_t ns = (row_pages + kAttnSplitPages - 1) / kAttnSplitPages;
   if (ns == 1) return;  // finished by the partition kernel
   const float* p = part + ((uint64_t)r * qh + head) * smax * kAttnPartialFloats;
-  // Lane s < ns holds partition s's (m, l).
-  const float ms = lane < (int)ns ? p[(uint64_t)lane * kAttnPartialFloats] : -__builtin_inff();
-  const float M = wave_max(ms);
-  const float ws = lane < (int)ns ? expf(ms - M) : 0.f;
-  const float lw = lane < (int)ns ? p[(uint64_t)lane * kAttnPartialFloats + 1] * ws : 0.f;
+  const float kNegInf = -__builtin_inff();
+  float mloc = kNegInf;
+  for (uint32_t sp = lane; sp < ns; sp += 64) mloc = fmaxf(mloc, p[(uint64_t)sp * kAttnPartialFloats]);
+  const float M = wave_max(mloc);
   float L = 0.f, n0 = 0.f, n1 = 0.f;
-  for (uint32_t s0 = 0; s0 < ns; s0 += 8) {
-    // Eight partitions' numerators in flight, then added in ascending order.
-    float a0[8], a1[8];
+  for (uint32_t c0 = 0; c0 < ns; c0 += 64) {
+    // Lane s holds partition c0 + s's weight exp(m - M) and weighted l.
+    const uint32_t mine = c0 + lane;
+    const float ms = mine < ns ? p[(uint64_t)mine * kAttnPartialFloats] : kNegInf;
+    const float ws = mine < ns ? expf(ms - M) : 0.f;
+    const float lw = mine < ns ? p[(uint64_t)mine * kAttnPartialFloats + 1] * ws : 0.f;
+    const uint32_t cn = min(64u, ns - c0);
+    for (uint32_t s0 = 0; s0 < cn; s0 += 8) {
+      // Eight partitions' numerators in flight, then added in ascending order.
+      float a0[8], a1[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t sp = s0 + u;
-      const float* ps = p + (uint64_t)sp * kAttnPartialFloats;
-      a0[u] = sp < ns ? ps[2 + 2 * lane] : 0.f;
-      a1[u] = sp < ns ? ps[3 + 2 * lane] : 0.f;
-    }
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t sp = s0 + u;
+        const float* ps = p + (uint64_t)(c0 + sp) * kAttnPartialFloats;
+        a0[u] = sp < cn ? ps[2 + 2 * lane] : 0.f;
+        a1[u] = sp < cn ? ps[3 + 2 * lane] : 0.f;
+      }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t sp = s0 + u;
-      if (sp < ns) {
-        const float w = lane_bcast(ws, (int)sp);
-        L += lane_bcast(lw, (int)sp);
-        n0 += a0[u] * w;
-        n1 += a1[u] * w;
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t sp = s0 + u;
+        if (sp < cn) {
+          const float w = lane_bcast(ws, (int)sp);
+          L += lane_bcast(lw, (int)sp);
+          n0 += a0[u] * w;
+          n1 += a1[u] * w;
+        }
       }
     }
   }
@@ -304,12 +368,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
   if (!(L > 0.f) || ((o0 & 0x7f80u) == 0x7f80u) || ((o1 & 0x7f80u) == 0x7f80u)) raise_error(err, ERR_NONFINITE);
 }
 
-template <int G>
+template <int G, int WAVES = 4>
 void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                       const uint32_t* table, float* part, uint16_t* out, uint32_t out_tiled, uint32_t rows,
                       uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t smax,
                       uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partition_kernel<G>), dim3(smax, kvh, rows), dim3(kAttnThreads), 0, s, q, kc, vc,
+  hipLaunchKernelGGL((attn_partition_kernel<G, WAVES>), dim3(smax, kvh, rows), dim3(64 * WAVES), 0, s, q, kc, vc,
                      positions, table, part, out, out_tiled, qh, kvh, stride, pages, context, smax, err);
 }
 

@@ -11,8 +11,8 @@ namespace fh {
 void set_thread_error(const char* msg);
 
 // Attention partition: each partition workgroup covers this many pages of
-// 16 tokens (8 per wave).
-constexpr uint32_t kAttnSplitPages = 32;
+// 16 tokens (every wave of the workgroup walks all of them for its KV head).
+constexpr uint32_t kAttnSplitPages = 16;
 constexpr uint32_t kAttnSplitTokens = kAttnSplitPages * 16;
 // Floats per attention partial record: running max, denominator, numerator[128].
 constexpr uint32_t kAttnPartialFloats = 2 + 128;
