@@ -203,10 +203,12 @@ def main():
         tokens, _ = step(tokens)
 
     step_byte_total = 0
+    device_ms = 0.0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tokens, positions = step(tokens)
+        device_ms += runner.last_step_ms()
         step_byte_total += step_bytes(cfg, batch, positions)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -246,6 +248,7 @@ def main():
         "config": {"workload": desc, "batch": batch, "contexts_mean": round(float(np.mean(contexts)), 1),
                    "decode_steps_timed": args.steps, "page_tokens": 16, "physical_pages": phys_pages,
                    "graphs": not args.eager, "profile_steps": args.profile_steps},
+        "device_ms_per_step": round(device_ms / args.steps, 4),  # HIP events around each step on the stream
         "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(step_gbs / PEAK_HBM_GBS, 4),
                      "bytes_per_step": int(step_byte_total / args.steps)},

@@ -12,16 +12,29 @@ slot before the call, and commits lengths after a successful step.
 from __future__ import annotations
 
 import random
-from dataclasses import dataclass, field
+
+import numpy as np
 
 from .runner import PAGE_TOKENS, PagedLimits, PreparedBatch, PreparedRow
 
 
-@dataclass
 class SequenceState:
-    sequence: int
-    length: int = 0  # committed tokens (KV positions 0..length-1 are written)
-    pages: list = field(default_factory=list)
+    """A sequence's committed length and its logical-to-physical page list,
+    kept as a uint32 array so a prepared row hands it to the C ABI as is."""
+
+    def __init__(self, sequence: int, capacity: int):
+        self.sequence = sequence
+        self.length = 0  # committed tokens (KV positions 0..length-1 are written)
+        self._table = np.zeros(capacity, dtype=np.uint32)
+        self._count = 0
+
+    @property
+    def pages(self) -> np.ndarray:
+        return self._table[: self._count]
+
+    def append_page(self, page: int) -> None:
+        self._table[self._count] = page
+        self._count += 1
 
 
 class PagePool:
@@ -39,7 +52,7 @@ class PagePool:
         """Admits a sequence whose first `prefix_tokens` KV positions are already resident."""
         sid = self._next_seq
         self._next_seq += 1
-        st = SequenceState(sid)
+        st = SequenceState(sid, self.limits.page_table_stride)
         self._ensure(st, prefix_tokens)
         st.length = prefix_tokens
         self.sequences[sid] = st
@@ -52,7 +65,7 @@ class PagePool:
         while len(st.pages) < need:
             if not self.free:
                 raise MemoryError("out of KV pages")
-            st.pages.append(self.free.pop())
+            st.append_page(self.free.pop())
 
     def prepare(self, rows: list) -> PreparedBatch:
         """rows: [(sequence, token)] in scheduler order; consecutive rows of one
@@ -64,10 +77,15 @@ class PagePool:
             pos = st.length + pending.get(sid, 0)
             pending[sid] = pending.get(sid, 0) + 1
             self._ensure(st, pos + 1)
-            prepared.append(PreparedRow(sid, int(token), pos, tuple(st.pages), st.pages[pos // PAGE_TOKENS]))
-        # Every row of a sequence sees the sequence's full reserved page list.
-        prepared = [PreparedRow(r.sequence, r.token, r.position, tuple(self.sequences[r.sequence].pages),
-                                r.writable_physical_page) for r in prepared]
+            prepared.append((sid, int(token), pos, int(st.pages[pos // PAGE_TOKENS])))
+        # Every row of a sequence sees the sequence's full reserved page list
+        # (a read-only copy: later growth of the sequence does not change it).
+        tables = {}
+        for sid in pending:
+            t = self.sequences[sid].pages.copy()
+            t.flags.writeable = False
+            tables[sid] = t
+        prepared = [PreparedRow(sid, token, pos, tables[sid], page) for sid, token, pos, page in prepared]
         bid = self._next_batch
         self._next_batch += 1
         return PreparedBatch(bid, prepared, self.limits)
@@ -79,4 +97,4 @@ class PagePool:
 
     def release(self, sid: int) -> None:
         st = self.sequences.pop(sid)
-        self.free.extend(st.pages)
+        self.free.extend(int(p) for p in st.pages)

@@ -46,7 +46,7 @@ class PreparedRow:
     sequence: int
     token: int
     position: int
-    physical_pages: tuple
+    physical_pages: Sequence[int]  # tuple, list or uint32 array
     writable_physical_page: int
 
     @property
@@ -76,19 +76,36 @@ def model_desc(cfg: dict) -> _lib.ModelDesc:
                           cfg["rms_epsilon"])
 
 
+# fh_row as a numpy record (layout checked against ctypes in the ABI tests).
+ROW_DTYPE = np.dtype([("sequence", "<u8"), ("token", "<u4"), ("position", "<u4"), ("pages", "<u8"),
+                      ("page_count", "<u4"), ("writable_page", "<u4")])
+
+
 def _rows_to_c(rows: Sequence[PreparedRow]):
-    arr = (_lib.Row * len(rows))()
-    keep = []
-    for i, r in enumerate(rows):
-        pages = np.ascontiguousarray(np.asarray(r.physical_pages, dtype=np.uint32))
+    """fh_row[] for the C ABI; returns (pointer, objects that must stay alive)."""
+    n = len(rows)
+    rec = np.zeros(max(n, 1), dtype=ROW_DTYPE)
+    keep = [rec]
+    seq, tok, pos, ptrs, cnt, wp = [], [], [], [], [], []
+    for r in rows:
+        pages = r.physical_pages
+        if not (isinstance(pages, np.ndarray) and pages.dtype == np.uint32 and pages.flags.c_contiguous):
+            pages = np.ascontiguousarray(np.asarray(pages, dtype=np.uint32))
         keep.append(pages)
-        arr[i].sequence = r.sequence
-        arr[i].token = r.token
-        arr[i].position = r.position
-        arr[i].pages = pages.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-        arr[i].page_count = len(pages)
-        arr[i].writable_page = r.writable_physical_page
-    return arr, keep
+        seq.append(r.sequence)
+        tok.append(r.token)
+        pos.append(r.position)
+        ptrs.append(pages.ctypes.data if len(pages) else 0)
+        cnt.append(len(pages))
+        wp.append(r.writable_physical_page)
+    if n:
+        rec["sequence"][:n] = seq
+        rec["token"][:n] = tok
+        rec["position"][:n] = pos
+        rec["pages"][:n] = ptrs
+        rec["page_count"][:n] = cnt
+        rec["writable_page"][:n] = wp
+    return ctypes.cast(rec.ctypes.data, ctypes.POINTER(_lib.Row)), keep
 
 
 class TpBatchRunner:

@@ -43,6 +43,10 @@ def test_struct_layouts_match_the_header():
     assert ctypes.sizeof(_lib.ModelDesc) == 10 * 4
     assert ctypes.sizeof(_lib.CtxOptions) == 7 * 4
     assert _lib.Row.pages.offset == 16 and ctypes.sizeof(_lib.Row) == 32
+    from ferric_amd.runner import ROW_DTYPE
+    assert ROW_DTYPE.itemsize == ctypes.sizeof(_lib.Row)
+    for name, _ in _lib.Row._fields_:
+        assert ROW_DTYPE.fields[name][1] == getattr(_lib.Row, name).offset, name
 
 
 def u32(a):
@@ -132,7 +136,7 @@ def test_page_pool_reserves_write_slots_and_consecutive_positions():
     batch = pool.prepare([(a, 7), (a, 8), (b, 9)])
     rows = batch.rows
     assert [r.position for r in rows] == [15, 16, 0]
-    assert rows[0].physical_pages == rows[1].physical_pages and len(rows[0].physical_pages) == 2
+    assert list(rows[0].physical_pages) == list(rows[1].physical_pages) and len(rows[0].physical_pages) == 2
     assert rows[0].writable_physical_page == rows[0].physical_pages[0]
     assert rows[1].writable_physical_page == rows[1].physical_pages[1]
     assert rows[1].writable_token_offset == 0
