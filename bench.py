@@ -43,6 +43,12 @@ WORKLOADS = {
     "qwen3-0.6b-b32": ("0.6b", 32, (128, 2048), 4608, 64,
                        "Qwen3-0.6B shape, batch-32 paged decode, ctx U[128,2048], shuffled page pool, greedy"),
 }
+# Prefill chunks: (model, sequences, prompt tokens, description)
+PREFILL_WORKLOADS = {
+    "qwen3-8b-prefill": ("8b", 32, 256, "Qwen3-8B shape, one chunked-prefill batch of 32 prompts x 256 random ids "
+                                        "from position 0 into a shuffled 16-token page pool; greedy first token"),
+}
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
 def parse():
@@ -50,7 +56,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=64)
     p.add_argument("--warmup", type=int, default=4)
-    p.add_argument("--workload", default="qwen3-8b-b32", choices=sorted(WORKLOADS))
+    p.add_argument("--workload", default="qwen3-8b-b32", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=2, help="decode steps the CPU oracle sample runs")
@@ -156,6 +162,94 @@ def cpu_baseline(cfg, contexts, args, seed):
         m.close()
 
 
+def prefill_flops(cfg, seqs, tokens):
+    """Algorithmic FLOPs of one prefill chunk: every projection for every
+    token, causal attention (QK^T and PV over keys 0..t), and the FP32 head
+    for each prompt's last token."""
+    H, QH, KVH, I, V, L = (cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["intermediate"],
+                           cfg["vocabulary"], cfg["layers"])
+    Q, KV = QH * 128, KVH * 128
+    linear = ((Q + 2 * KV) * H + H * Q + 3 * I * H) * 2  # per token per layer
+    keys = tokens * (tokens + 1) // 2  # causal key count per sequence
+    attn = keys * QH * 128 * 2 * 2  # QK^T + PV per sequence per layer
+    return L * (seqs * tokens * linear + seqs * attn) + seqs * V * H * 2
+
+
+def prefill_bench(args, name):
+    import torch
+
+    import ferric_amd
+    from ferric_amd import PagedLimits, PagePool, TpBatchRunner
+
+    model_key, seqs, tokens, desc = PREFILL_WORKLOADS[name]
+    cfg = dict(ferric_amd.QWEN3_8B if model_key == "8b" else ferric_amd.QWEN3_0_6B)
+    rows = seqs * tokens
+    context_tokens = (tokens + 15) // 16 * 16
+    pages_per_seq = context_tokens // 16
+    limits = PagedLimits(context_tokens=context_tokens, physical_page_count=seqs * pages_per_seq * 2,
+                         page_table_stride=pages_per_seq)
+    runner = TpBatchRunner(cfg, limits, row_capacity=32, use_graphs=False, prefill_rows=rows)
+    runner.synthesize_weights(args.seed, 0.02)
+    pool = PagePool(limits, seed=args.seed)
+    rng = np.random.default_rng(args.seed)
+    prompts = rng.integers(0, cfg["vocabulary"], (seqs, tokens))
+    outs = [(i + 1) * tokens - 1 for i in range(seqs)]
+
+    def step():
+        sids = [pool.admit(0) for _ in range(seqs)]
+        b = pool.prepare([(s, int(t)) for s, p in zip(sids, prompts) for t in p])
+        out = runner.execute_batch(b, outs)
+        for s in sids:
+            pool.release(s)
+        return out.choices
+
+    for _ in range(args.warmup):
+        step()
+    steps = max(1, min(args.steps, 8))
+    device_ms = 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+        device_ms += runner.last_step_ms()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    runner.set_profiling(True)
+    class_ms, class_launches = {}, {}
+    for _ in range(2):
+        step()
+        for k, (ms, n) in runner.kernel_class_ms().items():
+            class_ms[k] = class_ms.get(k, 0.0) + ms / 2
+            class_launches[k] = class_launches.get(k, 0) + n / 2
+    runner.set_profiling(False)
+    flops = prefill_flops(cfg, seqs, tokens)
+    tflops = flops / (elapsed / steps) / 1e12
+    H, QH, KVH, I = cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["intermediate"]
+    gemm_flops = {"qkv_gemm": rows * (QH + 2 * KVH) * 128 * H * 2, "o_gemm": rows * H * QH * 128 * 2,
+                  "gate_up_gemm": rows * 2 * I * H * 2, "down_gemm": rows * H * I * 2}
+    dominant = max(gemm_flops, key=lambda k: class_ms.get(k, 0.0))
+    avg_ms = class_ms[dominant] / max(class_launches[dominant], 1)
+    achieved = gemm_flops[dominant] / (avg_ms * 1e-3) / 1e12
+    result = {
+        "metric": f"prefill tokens/s and MFMA TFLOP/s, {desc}",
+        "value": round(rows * steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / steps, 3),
+        "device_ms_per_step": round(device_ms / steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": desc, "sequences": seqs, "prompt_tokens": tokens, "rows_per_chunk": rows},
+        "step_tflops": {"achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "flops_per_step": int(flops)},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_flops_per_launch": gemm_flops[dominant]},
+        "kernels": {k: {"ms_per_step": round(v, 3)} for k, v in sorted(class_ms.items(), key=lambda kv: -kv[1])},
+    }
+    runner.close()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -164,6 +258,10 @@ def main():
         sys.exit(2)
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+
+    if args.workload in PREFILL_WORKLOADS:
+        prefill_bench(args, args.workload)
         return
 
     import torch

@@ -84,16 +84,18 @@ __host__ __device__ __forceinline__ uint64_t tiled_offset(uint32_t n, uint32_t k
 }
 
 // Activation tile order: the B operand of the same MFMA for an activation
-// x[m][k] with m < 32 rows. Tile (kb, mt) holds rows 16*mt..16*mt+15 and
-// columns 32*kb..32*kb+31 as 64 lanes x 16 bytes (lane = m % 16 + 16 *
-// ((k % 32) / 8)); tiles are ordered kb-major, so a wave's B-operand load is
-// one contiguous 1 KiB. Producers of projection inputs (RMSNorm, the
-// attention output, the SwiGLU epilogue) write this order directly.
-__host__ __device__ __forceinline__ uint64_t act_offset(uint32_t m, uint32_t k) {
+// x[m][k]. Tile (kb, mt) holds rows 16*mt..16*mt+15 and columns
+// 32*kb..32*kb+31 as 64 lanes x 16 bytes (lane = m % 16 + 16 * ((k % 32) / 8));
+// tiles are ordered kb-major over `mtiles` row tiles, so a wave's B-operand
+// load is one contiguous 1 KiB. Producers of projection inputs (RMSNorm, the
+// attention output, the SwiGLU epilogue) write this order directly. Decode
+// buffers hold 32 rows (mtiles = 2); prefill buffers hold mtiles row tiles.
+__host__ __device__ __forceinline__ uint64_t act_offset_m(uint32_t m, uint32_t k, uint32_t mtiles) {
   const uint32_t kb = k >> 5, kk = k & 31u, mt = m >> 4;
   const uint32_t lane = (m & 15u) + 16u * (kk >> 3);
-  return ((((uint64_t)kb * 2 + mt) * 64u + lane) << 3) + (kk & 7u);
+  return ((((uint64_t)kb * mtiles + mt) * 64u + lane) << 3) + (kk & 7u);
 }
+__host__ __device__ __forceinline__ uint64_t act_offset(uint32_t m, uint32_t k) { return act_offset_m(m, k, 2); }
 
 // SwiGLU element in the stable-sigmoid form of qwen3_swiglu_element_v1
 // (device/qwen3-all-kernels-v1/src/swiglu.rs:62-101): e = exp(-|g|),

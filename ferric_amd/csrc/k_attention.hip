@@ -50,14 +50,16 @@ __device__ __forceinline__ float exp_fast(float x) {
 }
 
 // Stores one finished head output (dims 2*lane, 2*lane+1) in either layout.
-__device__ __forceinline__ void store_head(uint16_t* out, bool tiled, uint32_t r, uint32_t qh, uint32_t head, int lane,
-                                          uint32_t o0, uint32_t o1) {
+// Row r of the launch is row row0 + r of the output; the tiled layout has
+// out_mtiles row tiles (0: row-major [rows][qh * 128]).
+__device__ __forceinline__ void store_head(uint16_t* out, uint32_t out_mtiles, uint32_t row0, uint32_t r, uint32_t qh,
+                                          uint32_t head, int lane, uint32_t o0, uint32_t o1) {
   const uint32_t col = head * 128 + 2 * lane;
   const uint32_t word = o0 | (o1 << 16);
-  if (tiled)
-    *reinterpret_cast<uint32_t*>(out + act_offset(r, col)) = word;
+  if (out_mtiles)
+    *reinterpret_cast<uint32_t*>(out + act_offset_m(row0 + r, col, out_mtiles)) = word;
   else
-    reinterpret_cast<uint32_t*>(out + ((uint64_t)r * qh + head) * 128)[lane] = word;
+    reinterpret_cast<uint32_t*>(out + ((uint64_t)(row0 + r) * qh + head) * 128)[lane] = word;
 }
 
 // One workgroup per (partition, KV head, row); its WAVES waves split the
@@ -68,8 +70,8 @@ template <int G, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, float* __restrict__ part,
-    uint16_t* __restrict__ out, uint32_t out_tiled, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
-    uint32_t context, uint32_t smax, uint32_t* err) {
+    uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t row0, uint32_t qh, uint32_t kvh, uint32_t stride,
+    uint32_t pages, uint32_t context, uint32_t smax, uint32_t* err) {
   constexpr uint32_t kWavePages = kAttnSplitPages / WAVES;
   static_assert(kAttnSplitPages % WAVES == 0, "pages split evenly over the waves");
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
       }
       const uint32_t o0 = f32_to_bf16(n0 / L), o1 = f32_to_bf16(n1 / L);
       bad |= !(L > 0.f) | ((o0 & 0x7f80u) == 0x7f80u) | ((o1 & 0x7f80u) == 0x7f80u);
-      store_head(out, out_tiled != 0, r, qh, h * G + g, lane, o0, o1);
+      store_head(out, out_mtiles, row0, r, qh, h * G + g, lane, o0, o1);
     }
   } else {
     // Partition state (m, l, n[128]) of each query head.
@@ -316,9 +318,9 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
 
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* __restrict__ part,
                                                                   const uint32_t* __restrict__ positions,
-                                                                  uint16_t* __restrict__ out, uint32_t out_tiled,
-                                                                  uint32_t rows, uint32_t qh, uint32_t context,
-                                                                  uint32_t smax, uint32_t* err) {
+                                                                  uint16_t* __restrict__ out, uint32_t out_mtiles,
+                                                                  uint32_t row0, uint32_t rows, uint32_t qh,
+                                                                  uint32_t context, uint32_t smax, uint32_t* err) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t id = blockIdx.x * 4 + wave;
   const uint32_t r = id / qh, head = id % qh;
@@ -364,43 +366,46 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
     }
   }
   const uint32_t o0 = f32_to_bf16(n0 / L), o1 = f32_to_bf16(n1 / L);
-  store_head(out, out_tiled != 0, r, qh, head, lane, o0, o1);
+  store_head(out, out_mtiles, row0, r, qh, head, lane, o0, o1);
   if (!(L > 0.f) || ((o0 & 0x7f80u) == 0x7f80u) || ((o1 & 0x7f80u) == 0x7f80u)) raise_error(err, ERR_NONFINITE);
 }
 
 template <int G, int WAVES = 4>
 void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
-                      const uint32_t* table, float* part, uint16_t* out, uint32_t out_tiled, uint32_t rows,
-                      uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t smax,
-                      uint32_t* err, hipStream_t s) {
+                      const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
+                      uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                      uint32_t smax, uint32_t* err, hipStream_t s) {
   hipLaunchKernelGGL((attn_partition_kernel<G, WAVES>), dim3(smax, kvh, rows), dim3(64 * WAVES), 0, s, q, kc, vc,
-                     positions, table, part, out, out_tiled, qh, kvh, stride, pages, context, smax, err);
+                     positions, table, part, out, out_mtiles, row0, qh, kvh, stride, pages, context, smax, err);
 }
 
 }  // namespace
 
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
-                                    uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride,
-                                    uint32_t pages, uint32_t context, uint32_t* err, hipStream_t s) {
+                                    uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
+                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t* err,
+                                    hipStream_t s) {
   const uint32_t smax = attn_max_splits(context);
+  const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   switch (qh / kvh) {
-    case 1: launch_partition<1>(q, k_cache, v_cache, positions, table, partials, out, out_tiled, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 2: launch_partition<2>(q, k_cache, v_cache, positions, table, partials, out, out_tiled, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 4: launch_partition<4>(q, k_cache, v_cache, positions, table, partials, out, out_tiled, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 8: launch_partition<8>(q, k_cache, v_cache, positions, table, partials, out, out_tiled, rows, qh, kvh, stride, pages, context, smax, err, s); break;
+    case 1: launch_partition<1>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
+    case 2: launch_partition<2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
+    case 4: launch_partition<4>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
+    case 8: launch_partition<8>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
-                                  uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t context, uint32_t* err,
-                                  hipStream_t s) {
+                                  uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
+                                  uint32_t context, uint32_t* err, hipStream_t s) {
   const uint32_t smax = attn_max_splits(context);
   const uint32_t waves = rows * qh;
+  const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   hipLaunchKernelGGL(attn_merge_kernel, dim3((waves + 3) / 4), dim3(kAttnThreads), 0, s, partials, positions, out,
-                     out_tiled, rows, qh, context, smax, err);
+                     mt, row0, rows, qh, context, smax, err);
   return hipGetLastError();
 }
 

@@ -1,0 +1,169 @@
+// K1 projections for prefill and wide verify batches (m > 32 token rows):
+// bf16 MFMA (v_mfma_f32_16x16x32_bf16), FP32 accumulation, compute-bound.
+//
+// Operands come straight from their tile orders (common.hpp): the weight in
+// weight tile order and the activation in activation tile order with
+// act_mtiles(m) row tiles, so every operand load of a wave is one contiguous
+// 1 KiB that lands in MFMA registers. A workgroup of 4 waves computes a
+// 128 (n) x 128 (m) block: waves 0/1 and 2/3 share m rows, waves 0/2 and 1/3
+// share n rows, so each operand tile is fetched by two waves of the block
+// (the second fetch hits the CU's cache). Each wave accumulates 4 x 4 MFMA
+// tiles over the whole k range, with the next k-block's operands in flight.
+//
+// Epilogues (same rounding points as the decode kernel, no split-K here):
+//   FH_EPI_BF16     out[m][n] = bf16(acc)
+//   FH_EPI_RESIDUAL out[m][n] = bf16((0 + acc) + residual[m][n]) (may alias out)
+//   FH_EPI_SWIGLU   act = swiglu(bf16(gate), bf16(up)) in activation tile order
+//                   (gate/up tiles interleaved by the weight layout)
+//   FH_EPI_F32      out[m][n] = acc (FP32 logits)
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../../include/ferric_hip.h"
+
+namespace fh {
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kNT = 4;  // n-tiles per wave
+constexpr int kMT = 4;  // m-tiles per wave
+constexpr int kBlockTiles = 2 * kNT;  // 16-row tiles per block side (128 rows)
+static_assert(kLargeBlockRows == 16 * 2 * kMT, "block rows match the wave layout");
+
+__device__ __forceinline__ bf16x8 b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_large_kernel(const uint16_t* __restrict__ xt,
+                                                         const uint16_t* __restrict__ w, uint32_t m,
+                                                         uint32_t mtiles, uint32_t kb_count,
+                                                         const uint16_t* residual, void* out, uint32_t ldo,
+                                                         uint32_t out_mtiles) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t nt0 = blockIdx.x * kBlockTiles + (wave & 1) * kNT;  // first 16-row weight tile
+  const uint32_t mt0 = blockIdx.y * kBlockTiles + (wave >> 1) * kMT;  // first 16-row activation tile
+  if (mt0 * 16 >= m) return;  // this wave's rows are all padding
+
+  // Per k-block: weight tile (nb, kb) at (nb * kb_count + kb) KiB; activation
+  // tile (kb, mt) at (kb * mtiles + mt) KiB. Pointers are in 16-byte units.
+  const u32x4* wp = reinterpret_cast<const u32x4*>(w) + (uint64_t)nt0 * kb_count * 64 + lane;
+  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)mt0 * 64 + lane;
+  const uint64_t w_tile_stride = (uint64_t)kb_count * 64;  // next n-tile
+  const uint64_t x_kb_stride = (uint64_t)mtiles * 64;      // next k-block
+
+  f32x4 acc[kNT][kMT];
+#pragma unroll
+  for (int i = 0; i < kNT; ++i)
+#pragma unroll
+    for (int j = 0; j < kMT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 wa[kNT], xa[kMT], wb[kNT], xb[kMT];
+  auto load = [&](u32x4(&wv)[kNT], u32x4(&xv)[kMT], uint32_t kb) {
+#pragma unroll
+    for (int i = 0; i < kNT; ++i) wv[i] = wp[i * w_tile_stride + kb * 64];
+#pragma unroll
+    for (int j = 0; j < kMT; ++j) xv[j] = xp[kb * x_kb_stride + j * 64];
+  };
+  auto compute = [&](const u32x4(&wv)[kNT], const u32x4(&xv)[kMT]) {
+#pragma unroll
+    for (int i = 0; i < kNT; ++i)
+#pragma unroll
+      for (int j = 0; j < kMT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(wv[i]), b8(xv[j]), acc[i][j], 0, 0, 0);
+  };
+  load(wa, xa, 0);
+  for (uint32_t kb = 0; kb < kb_count; kb += 2) {
+    if (kb + 1 < kb_count) load(wb, xb, kb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(wa, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kb + 1 < kb_count) {
+      if (kb + 2 < kb_count) load(wa, xa, kb + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb, xb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // D layout: lane l, element e holds weight row n = 16 nt + 4 (l / 16) + e
+  // and activation row m = 16 mt + l % 16.
+  const uint32_t q = lane >> 4, c = lane & 15;
+  if constexpr (EPI == FH_EPI_SWIGLU) {
+    static_assert(kNT % 2 == 0, "gate/up tile pairs");
+    bool bad = false;
+#pragma unroll
+    for (int p = 0; p < kNT / 2; ++p) {
+      const uint32_t col = ((nt0 + 2 * p) / 2) * 16 + 4 * q;  // first of 4 output columns
+#pragma unroll
+      for (int j = 0; j < kMT; ++j) {
+        const uint32_t row = (mt0 + j) * 16 + c;
+        if (row >= m) continue;
+        uint32_t y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = swiglu_bf16(round_bf16(acc[2 * p][j][e]), round_bf16(acc[2 * p + 1][j][e]), bad);
+        uint2 v = make_uint2(y[0] | (y[1] << 16), y[2] | (y[3] << 16));
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + act_offset_m(row, col, out_mtiles)) = v;
+      }
+    }
+    (void)bad;  // a nonfinite activation surfaces at the next residual + norm
+  } else {
+#pragma unroll
+    for (int i = 0; i < kNT; ++i) {
+      const uint32_t n = (nt0 + i) * 16 + 4 * q;
+#pragma unroll
+      for (int j = 0; j < kMT; ++j) {
+        const uint32_t row = (mt0 + j) * 16 + c;
+        if (row >= m) continue;
+        const uint64_t o = (uint64_t)row * ldo + n;
+        if constexpr (EPI == FH_EPI_F32) {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + o) = acc[i][j];
+        } else if constexpr (EPI == FH_EPI_BF16) {
+          uint2 v = make_uint2(f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16),
+                               f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16));
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = v;
+        } else {
+          const uint2 rv = *reinterpret_cast<const uint2*>(residual + o);
+          const float r0 = lo_bf16(rv.x), r1 = hi_bf16(rv.x), r2 = lo_bf16(rv.y), r3 = hi_bf16(rv.y);
+          uint2 v = make_uint2(f32_to_bf16((0.0f + acc[i][j][0]) + r0) | (f32_to_bf16((0.0f + acc[i][j][1]) + r1) << 16),
+                               f32_to_bf16((0.0f + acc[i][j][2]) + r2) | (f32_to_bf16((0.0f + acc[i][j][3]) + r3) << 16));
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = v;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+  if (n % (16 * kBlockTiles) != 0 || k % 32 != 0 || m == 0) return hipErrorInvalidValue;
+  const uint32_t mtiles = act_mtiles(m);
+  const uint32_t out_mtiles = epilogue == FH_EPI_SWIGLU ? act_mtiles(m) : 0u;
+  const dim3 grid(n / (16 * kBlockTiles), mtiles / kBlockTiles);
+  const uint32_t kb = k / 32;
+  switch (epilogue) {
+    case FH_EPI_BF16:
+      hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_BF16>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
+                         residual, out, ldo, out_mtiles);
+      break;
+    case FH_EPI_RESIDUAL:
+      hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_RESIDUAL>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
+                         residual, out, ldo, out_mtiles);
+      break;
+    case FH_EPI_SWIGLU:
+      hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_SWIGLU>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
+                         residual, out, ldo, out_mtiles);
+      break;
+    case FH_EPI_F32:
+      hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_F32>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
+                         residual, out, ldo, out_mtiles);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fh

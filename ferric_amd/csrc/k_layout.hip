@@ -134,6 +134,16 @@ __global__ __launch_bounds__(kThreads) void kv_fill_kernel(uint16_t* __restrict_
   }
 }
 
+// dst[i][:] = src[index[i]][:] for i < rows (width % 8 == 0), one workgroup per row.
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint16_t* __restrict__ src,
+                                                               const uint32_t* __restrict__ index,
+                                                               uint16_t* __restrict__ dst, uint32_t width) {
+  const uint32_t row = blockIdx.x;
+  const uint4* s = reinterpret_cast<const uint4*>(src + (uint64_t)index[row] * width);
+  uint4* d = reinterpret_cast<uint4*>(dst + (uint64_t)row * width);
+  for (uint32_t c = threadIdx.x; c < width / 8; c += kThreads) d[c] = s[c];
+}
+
 __global__ void clear_word_kernel(uint32_t* word) {
   if (threadIdx.x == 0) *word = 0u;
 }
@@ -186,6 +196,12 @@ hipError_t launch_kv_fill(uint16_t* cache, const uint32_t* table, const uint32_t
   uint64_t chunks = (uint64_t)max_length * kv_heads * 128 / 8;
   hipLaunchKernelGGL(kv_fill_kernel, dim3(grid_for(chunks, kThreads, 4096), rows), dim3(kThreads), 0, s, cache, table,
                      lengths, keys, stride, kv_heads, tensor_seed, scale, context_stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const uint16_t* src, const uint32_t* index, uint16_t* dst, uint32_t rows,
+                              uint32_t width, hipStream_t s) {
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(rows), dim3(kThreads), 0, s, src, index, dst, width);
   return hipGetLastError();
 }
 

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
                                                                         const float* __restrict__ part,
                                                                         uint32_t splits,
                                                                         const uint16_t* __restrict__ w,
-                                                                        uint16_t* __restrict__ y, uint32_t y_tiled,
+                                                                        uint16_t* __restrict__ y, uint32_t y_mtiles,
                                                                         uint32_t width, float eps, uint32_t* err) {
   __shared__ float red[kNormThreads / 64];
   const uint32_t row = blockIdx.x;
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
         o[q] = a | (b << 16);
       }
       const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
-      if (y_tiled)
-        *reinterpret_cast<uint4*>(y + act_offset(row, c * 8)) = ov;
+      if (y_mtiles)
+        *reinterpret_cast<uint4*>(y + act_offset_m(row, c * 8, y_mtiles)) = ov;
       else
         *reinterpret_cast<uint4*>(y + (uint64_t)row * width + c * 8) = ov;
     }
@@ -316,16 +316,17 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
 // Row-major <-> activation tile order, one 16-byte chunk per thread.
 __global__ __launch_bounds__(kNormThreads) void tile_activation_kernel(const uint16_t* __restrict__ x,
                                                                        uint16_t* __restrict__ xt, uint32_t m,
-                                                                       uint32_t k, uint32_t to_tiled) {
+                                                                       uint32_t k, uint32_t to_tiled,
+                                                                       uint32_t mtiles) {
   const uint32_t chunks = m * (k / 8);
   for (uint32_t c = blockIdx.x * kNormThreads + threadIdx.x; c < chunks; c += gridDim.x * kNormThreads) {
     const uint32_t row = c / (k / 8), col = (c % (k / 8)) * 8;
     if (to_tiled)
-      *reinterpret_cast<uint4*>(xt + act_offset(row, col)) =
+      *reinterpret_cast<uint4*>(xt + act_offset_m(row, col, mtiles)) =
           *reinterpret_cast<const uint4*>(x + (uint64_t)row * k + col);
     else
       *reinterpret_cast<uint4*>(const_cast<uint16_t*>(x) + (uint64_t)row * k + col) =
-          *reinterpret_cast<const uint4*>(xt + act_offset(row, col));
+          *reinterpret_cast<const uint4*>(xt + act_offset_m(row, col, mtiles));
   }
 }
 
@@ -376,7 +377,7 @@ hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint
                                    uint32_t* err, hipStream_t s) {
 #define FH_RESNORM(S_)                                                                                             \
   hipLaunchKernelGGL(residual_rmsnorm_kernel<S_>, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, \
-                     y, y_tiled, width, eps, err)
+                     y, y_tiled ? act_mtiles(rows) : 0u, width, eps, err)
   switch (partials ? splits : 0) {
     case 0: FH_RESNORM(0); break;
     case 1: FH_RESNORM(1); break;
@@ -396,7 +397,7 @@ hipError_t launch_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t
   const uint32_t chunks = m * (k / 8);
   const uint32_t grid = (chunks + kNormThreads - 1) / kNormThreads;
   hipLaunchKernelGGL(tile_activation_kernel, dim3(grid ? grid : 1), dim3(kNormThreads), 0, s, x, x_tiled, m, k,
-                     to_tiled);
+                     to_tiled, act_mtiles(m));
   return hipGetLastError();
 }
 

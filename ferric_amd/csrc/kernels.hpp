@@ -21,6 +21,13 @@ constexpr uint32_t kArgmaxShards = 64;
 // Token rows of one decode step (the activation tile order holds 2 m-tiles);
 // split-K partial slabs are [kMaxRows][n] FP32.
 constexpr uint32_t kMaxRows = 32;
+// Prefill / wide batches (m > kMaxRows rows) run the large GEMM, whose
+// workgroups cover 128 activation rows; their activation buffers hold
+// act_mtiles(m) 16-row tiles (decode buffers: 2).
+constexpr uint32_t kLargeBlockRows = 128;
+inline uint32_t act_mtiles(uint32_t m) {
+  return m <= kMaxRows ? 2u : ((m + kLargeBlockRows - 1) / kLargeBlockRows) * (kLargeBlockRows / 16);
+}
 
 inline uint32_t attn_max_splits(uint32_t context_tokens) {
   return (context_tokens + kAttnSplitTokens - 1) / kAttnSplitTokens;
@@ -37,6 +44,9 @@ hipError_t launch_fill_u16(uint16_t* dst, uint64_t count, uint16_t value, hipStr
 hipError_t launch_kv_fill(uint16_t* cache, const uint32_t* table, const uint32_t* lengths, const uint64_t* keys,
                           uint32_t rows, uint32_t stride, uint32_t kv_heads, uint64_t tensor_seed, float scale,
                           uint32_t context_stride, uint32_t max_length, hipStream_t s);
+// dst[i] = src[index[i]] for i < rows; rows of `width` bf16 (width % 8 == 0).
+hipError_t launch_gather_rows(const uint16_t* src, const uint32_t* index, uint16_t* dst, uint32_t rows,
+                              uint32_t width, hipStream_t s);
 hipError_t launch_clear_word(uint32_t* word, hipStream_t s);
 hipError_t launch_copy_u16(const uint16_t* src, uint16_t* dst, uint64_t count, hipStream_t s);
 
@@ -58,6 +68,9 @@ hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out
                          hipStream_t s);
 
 // projections
+// m > kMaxRows: no split-K; n % 128 == 0; x in activation tile order with act_mtiles(m) tiles.
+hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s);
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        hipStream_t s);
@@ -65,13 +78,17 @@ uint32_t gemm_default_splits(uint32_t n, uint32_t k);
 
 // attention
 // out: [rows][qh*128] row-major, or activation tile order when out_tiled.
+// Rows [0, rows) of a launch are rows row0 + [0, rows) of an output of
+// out_rows rows (activation tile order with act_mtiles(out_rows) tiles when
+// out_tiled, else row-major); q/positions/table/partials are the launch's own.
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
-                                    uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride,
-                                    uint32_t pages, uint32_t context, uint32_t* err, hipStream_t s);
+                                    uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
+                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t* err,
+                                    hipStream_t s);
 hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
-                                  uint32_t out_tiled, uint32_t rows, uint32_t qh, uint32_t context, uint32_t* err,
-                                  hipStream_t s);
+                                  uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
+                                  uint32_t context, uint32_t* err, hipStream_t s);
 
 // logits
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,

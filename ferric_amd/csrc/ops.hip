@@ -63,8 +63,7 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
 fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                      uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                      void* stream) {
-  if (!x_tiled || !w_tiled || !out || m == 0 || m > fh::kMaxRows || n == 0 || k == 0 || n % 16 || k % 32)
-    return FH_ERR_INVALID_ARGUMENT;
+  if (!x_tiled || !w_tiled || !out || m == 0 || n == 0 || k == 0 || n % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue > FH_EPI_PARTIAL || splits == 0 || splits > k / 32) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue != FH_EPI_PARTIAL && splits != 1) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue == FH_EPI_RESIDUAL && !residual) return FH_ERR_INVALID_ARGUMENT;
@@ -73,18 +72,26 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
   } else if (ldo < n) {
     return FH_ERR_INVALID_ARGUMENT;
   }
+  if (m > fh::kMaxRows) {
+    // Prefill-size batches: 128 x 128 blocks, no split-K, 8-byte aligned rows.
+    if (epilogue == FH_EPI_PARTIAL || n % (16 * 8) || (epilogue != FH_EPI_SWIGLU && ldo % 4))
+      return FH_ERR_INVALID_ARGUMENT;
+    return from_hip(fh::launch_gemm_large(x_tiled, w_tiled, m, n, k, epilogue, residual, out, ldo, as_stream(stream)));
+  }
   return from_hip(fh::launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, splits, residual, out, ldo, as_stream(stream)));
 }
+
+uint32_t fh_activation_rows(uint32_t m) { return m ? fh::act_mtiles(m) * 16 : 0u; }
 
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k) { return fh::gemm_default_splits(n, k); }
 
 fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream) {
-  if (!x || !x_tiled || m == 0 || m > fh::kMaxRows || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  if (!x || !x_tiled || m == 0 || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
   return from_hip(fh::launch_tile_activation(x, x_tiled, m, k, 1, as_stream(stream)));
 }
 
 fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t m, uint32_t k, void* stream) {
-  if (!x || !x_tiled || m == 0 || m > fh::kMaxRows || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
+  if (!x || !x_tiled || m == 0 || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
   return from_hip(fh::launch_tile_activation(x, const_cast<uint16_t*>(x_tiled), m, k, 0, as_stream(stream)));
 }
 
@@ -93,7 +100,6 @@ fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32
                                  uint32_t* error_word, void* stream) {
   if (!hidden || !weight || !y || rows == 0 || width == 0 || width % 32 || width > 8192 || (splits && !partials))
     return FH_ERR_INVALID_ARGUMENT;
-  if (y_tiled && rows > fh::kMaxRows) return FH_ERR_INVALID_ARGUMENT;
   if (splits && rows > fh::kMaxRows) return FH_ERR_INVALID_ARGUMENT;
   return from_hip(fh::launch_residual_rmsnorm(hidden, partials, splits, weight, y, y_tiled, rows, width, epsilon,
                                               error_word, as_stream(stream)));
@@ -127,18 +133,20 @@ fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, cons
                                 uint32_t* error_word, void* stream) {
   if (!q || !k_cache || !v_cache || !positions || !page_table || !out || !scratch || rows == 0 || kv_heads == 0 ||
       query_heads % kv_heads != 0 || stride == 0 || physical_pages == 0 || context_tokens == 0 ||
-      (uint64_t)stride * 16 < context_tokens || (out_tiled && rows > fh::kMaxRows))
+      (uint64_t)stride * 16 < context_tokens)
     return FH_ERR_INVALID_ARGUMENT;
   const uint32_t g = query_heads / kv_heads;
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
   hipStream_t s = as_stream(stream);
   float* part = reinterpret_cast<float*>(scratch);
-  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, rows,
-                                              query_heads, kv_heads, stride, physical_pages, context_tokens,
-                                              error_word, s);
+  (void)hipGetLastError();
+  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,
+                                              rows, rows, query_heads, kv_heads, stride, physical_pages,
+                                              context_tokens, error_word, s);
   if (e == hipSuccess)
-    e = fh::launch_attention_merge(part, positions, out, out_tiled, rows, query_heads, context_tokens, error_word, s);
-  return from_hip(e);
+    e = fh::launch_attention_merge(part, positions, out, out_tiled, 0, rows, rows, query_heads, context_tokens,
+                                   error_word, s);
+  return status_of(e);
 }
 
 fh_status fh_op_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t elements,

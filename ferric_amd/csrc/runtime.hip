@@ -25,6 +25,10 @@ namespace {
 constexpr uint32_t kNoLayer = 0xffffffffu;  // QWEN3_NO_LAYER, crates/ferric-spec/src/qwen3.rs:12
 constexpr uint32_t kPageTokens = 16;
 constexpr uint32_t kMaxRows = 32;
+// Prefill chunks: attention runs over this many rows per launch pair (bounds
+// the partition-state scratch), and at most this many output rows get logits.
+constexpr uint32_t kPrefillAttnRows = 256;
+constexpr uint32_t kMaxPrefillOutputs = 256;
 
 thread_local std::string g_create_error;
 
@@ -86,6 +90,28 @@ struct fh_ctx {
   uint32_t* h_meta = nullptr;  // pinned mirror
   uint32_t* h_out = nullptr;   // pinned: choices[cap] | error word
 
+  // Prefill chunks (row_capacity < rows <= prefill_rows); allocated only when
+  // prefill_rows > 0. Activation-tile buffers hold act_mtiles(prefill_rows) tiles.
+  struct Prefill {
+    uint16_t* hidden = nullptr;    // [rows][hidden]
+    uint16_t* xn = nullptr;        // tiled
+    uint16_t* qkv = nullptr;       // [rows][nqkv]
+    uint16_t* qrot = nullptr;      // [rows][qh*128]
+    uint16_t* attn = nullptr;      // tiled
+    uint16_t* act = nullptr;       // tiled
+    float* attn_part = nullptr;    // partition states of kPrefillAttnRows rows
+    uint16_t* out_hidden = nullptr;  // gathered output rows [kMaxPrefillOutputs][hidden]
+    uint16_t* out_xn = nullptr;    // tiled
+    float* logits = nullptr;       // [kMaxPrefillOutputs][vocab]
+    void* argmax_scratch = nullptr;
+    uint32_t* choices = nullptr;
+    uint32_t* d_meta = nullptr;    // tokens[P] | positions[P] | output rows[kMaxPrefillOutputs] | table[P][stride]
+    uint32_t* h_meta = nullptr;
+    uint32_t* h_out = nullptr;     // choices[kMaxPrefillOutputs] | error word
+  } pre;
+  const float* last_logits = nullptr;  // what fh_read_logits copies
+  bool last_was_prefill = false;
+
   uint32_t nqkv = 0;
   std::vector<uint8_t> have;  // which tensors are resident
   bool poisoned = false;
@@ -112,6 +138,7 @@ struct fh_ctx {
   std::vector<uint32_t> page_logical;
   std::vector<uint8_t> page_conflict;
   std::vector<uint64_t> row_stamp;
+  std::vector<uint64_t> slot_scratch;
   uint64_t stamp = 0;
 };
 
@@ -254,8 +281,11 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
   if (ctx->poisoned)
     return fail(ctx, FH_ERR_POISONED, "batched execution is closed, poisoned, or missing its v8 head profile");
   if (!all_weights_present(ctx)) return fail(ctx, FH_ERR_STATE, "model weights are not resident");
-  if (batch_id <= ctx->last_batch || nrows == 0 || nrows > ctx->opt.row_capacity || rows == nullptr)
+  const uint32_t max_rows = std::max(ctx->opt.row_capacity, ctx->opt.prefill_rows);
+  if (batch_id <= ctx->last_batch || nrows == 0 || nrows > max_rows || rows == nullptr)
     return fail(ctx, FH_ERR_INVALID_BATCH, "foreign, stale, or invalid prepared GPU batch");
+  if (nrows > ctx->opt.row_capacity && nout > kMaxPrefillOutputs)
+    return fail(ctx, FH_ERR_OUTPUT_ROWS, "output rows must be unique, ascending, and within the batch");
   const uint32_t P = ctx->opt.physical_pages, stride = ctx->opt.page_table_stride;
   const uint64_t gen = ++ctx->stamp;
   // Pass 1: page -> (sequence, logical) ownership over every row's list.
@@ -277,29 +307,29 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
     }
   }
   // Pass 2: per-row geometry, unique pages, unique write slots.
-  std::vector<uint64_t> slots;
-  slots.reserve(nrows);
+  std::vector<uint64_t>& slots = ctx->slot_scratch;
+  slots.clear();
   for (uint32_t i = 0; i < nrows; ++i) {
     const fh_row& r = rows[i];
     const uint32_t logical = r.position / kPageTokens;
     if (r.position >= ctx->opt.context_tokens || r.token >= ctx->md.vocabulary || logical >= r.page_count ||
         r.pages[logical] != r.writable_page)
       return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
-    const uint64_t row_gen = (gen << 6) | i;
+    const uint64_t row_gen = (gen << 16) | i;  // i < 16384
     for (uint32_t j = 0; j < r.page_count; ++j) {
       const uint32_t pg = r.pages[j];
       if (ctx->row_stamp[pg] == row_gen)
         return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
       ctx->row_stamp[pg] = row_gen;
     }
-    const uint64_t slot = (uint64_t)r.pages[logical] * kPageTokens + r.position % kPageTokens;
-    if (std::find(slots.begin(), slots.end(), slot) != slots.end())
-      return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
-    slots.push_back(slot);
+    slots.push_back((uint64_t)r.pages[logical] * kPageTokens + r.position % kPageTokens);
     const uint32_t wp = r.pages[logical];
     if (ctx->page_conflict[wp] || ctx->page_seq[wp] != r.sequence || ctx->page_logical[wp] != logical)
       return fail(ctx, FH_ERR_SHARED_PAGE, "batch writes a page shared with another sequence or logical position");
   }
+  std::sort(slots.begin(), slots.end());
+  if (std::adjacent_find(slots.begin(), slots.end()) != slots.end())
+    return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
   for (uint32_t i = 0; i < nout; ++i)
     if (output_rows[i] >= nrows || (i > 0 && output_rows[i] <= output_rows[i - 1]))
       return fail(ctx, FH_ERR_OUTPUT_ROWS, "output rows must be unique, ascending, and within the batch");
@@ -379,11 +409,11 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
                                        d_tab, ctx->qrot, kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon, err, s);
     });
     L(FH_KC_ATTENTION, [&] {
-      return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, ctx->attn, 1, R, QH, KVH,
-                                          stride, P, C, err, s);
+      return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, ctx->attn, 1, 0, R, R, QH,
+                                          KVH, stride, P, C, err, s);
     });
     L(FH_KC_ATTENTION_MERGE, [&] {
-      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, R, QH, C, err, s);
+      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, 0, R, R, QH, C, err, s);
     });
     L(FH_KC_O_GEMM, [&] {
       return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, s);
@@ -420,6 +450,19 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   return q.first_error;
 }
 
+void collect_profile(fh_ctx* ctx) {
+  for (uint32_t c = 0; c < FH_KC_COUNT; ++c) {
+    ctx->class_ms[c] = 0.f;
+    ctx->class_launches[c] = 0;
+  }
+  for (const auto& pl : ctx->prof_launches) {
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, pl.begin, pl.end);
+    ctx->class_ms[pl.cls] += ms;
+    ctx->class_launches[pl.cls] += 1;
+  }
+}
+
 std::string error_bits(uint32_t e) {
   std::string s;
   if (e & fh::ERR_NONFINITE) s += " nonfinite-value";
@@ -451,8 +494,11 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
       md.vocabulary == 0 || (md.query_heads * 128) % 256 != 0 || md.query_heads + md.kv_heads > 64)
     return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "unsupported model shape");
   if (op.row_capacity == 0 || op.row_capacity > kMaxRows || op.physical_pages == 0 || op.context_tokens == 0 ||
-      op.page_table_stride == 0 || op.page_table_stride * kPageTokens < op.context_tokens)
+      op.page_table_stride == 0 || op.page_table_stride * kPageTokens < op.context_tokens ||
+      (op.prefill_rows != 0 && (op.prefill_rows <= op.row_capacity || op.prefill_rows > 16384)))
     return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "unsupported context options");
+  if (op.prefill_rows && md.vocabulary % 128 != 0)
+    return fail(nullptr, FH_ERR_INVALID_ARGUMENT, "unsupported model shape for prefill (vocabulary % 128)");
 
   fh_ctx* ctx = new fh_ctx();
   ctx->md = md;
@@ -524,6 +570,35 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   TRY(dalloc(ctx, &ctx->d_meta, meta));
   TRY(halloc(ctx, &ctx->h_meta, meta));
   TRY(halloc(ctx, &ctx->h_out, cap + 1));
+  if (op.prefill_rows) {
+    auto& p = ctx->pre;
+    const uint32_t P = op.prefill_rows;
+    const uint64_t tiled_rows = (uint64_t)fh::act_mtiles(P) * 16;
+    const uint64_t out_tiled_rows = (uint64_t)fh::act_mtiles(kMaxPrefillOutputs) * 16;
+    TRY(dalloc(ctx, &p.hidden, (uint64_t)P * H));
+    TRY(dalloc(ctx, &p.xn, tiled_rows * H));
+    TRY(dalloc(ctx, &p.qkv, (uint64_t)P * ctx->nqkv));
+    TRY(dalloc(ctx, &p.qrot, (uint64_t)P * Q));
+    TRY(dalloc(ctx, &p.attn, tiled_rows * Q));
+    TRY(dalloc(ctx, &p.act, tiled_rows * I));
+    TRY(dalloc(ctx, &p.attn_part, (uint64_t)kPrefillAttnRows * md.query_heads * fh::attn_max_splits(op.context_tokens) *
+                                      fh::kAttnPartialFloats));
+    TRY(dalloc(ctx, &p.out_hidden, (uint64_t)kMaxPrefillOutputs * H));
+    TRY(dalloc(ctx, &p.out_xn, out_tiled_rows * H));
+    TRY(dalloc(ctx, &p.logits, (uint64_t)kMaxPrefillOutputs * V));
+    TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&p.argmax_scratch), fh_argmax_scratch_bytes(kMaxPrefillOutputs)));
+    TRY(dalloc(ctx, &p.choices, kMaxPrefillOutputs));
+    const uint64_t pmeta = 2ull * P + kMaxPrefillOutputs + (uint64_t)P * op.page_table_stride;
+    TRY(dalloc(ctx, &p.d_meta, pmeta));
+    TRY(halloc(ctx, &p.h_meta, pmeta));
+    TRY(halloc(ctx, &p.h_out, kMaxPrefillOutputs + 1));
+    // Padding rows of the tiled buffers are read (never used) by the GEMM.
+    e = fh::launch_fill_u16(p.xn, tiled_rows * H, 0, ctx->stream);
+    if (e == hipSuccess) e = fh::launch_fill_u16(p.attn, tiled_rows * Q, 0, ctx->stream);
+    if (e == hipSuccess) e = fh::launch_fill_u16(p.act, tiled_rows * I, 0, ctx->stream);
+    if (e == hipSuccess) e = fh::launch_fill_u16(p.out_xn, out_tiled_rows * H, 0, ctx->stream);
+    if (e != hipSuccess) return bail(hip_fail(ctx, e, "initialising prefill buffers"));
+  }
 
   // RoPE table exactly as rope_bytes (tp_execution.rs:1440-1450): f64
   // theta^(-pair/64), angle = position * inverse_frequency, cos/sin in f64,
@@ -730,12 +805,139 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
   return FH_OK;
 }
 
+// A prefill chunk (row_capacity < nrows <= prefill_rows), launched eagerly:
+// the decode path's op order (batched.rs:1746-2454) with the compute-bound
+// projections, bf16 QKV rows into the QK-norm kernel, attention in row
+// blocks of kPrefillAttnRows, and the final norm + FP32 head + argmax over
+// the requested output rows only.
+fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                      const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
+  const fh_model_desc& md = ctx->md;
+  const fh_ctx_options& op = ctx->opt;
+  auto& p = ctx->pre;
+  const uint32_t P = op.prefill_rows, stride = op.page_table_stride;
+  const uint32_t H = md.hidden, QH = md.query_heads, KVH = md.kv_heads, Q = QH * 128, I = md.intermediate,
+                 V = md.vocabulary, C = op.context_tokens, pages = op.physical_pages;
+  uint32_t* tok = p.h_meta;
+  uint32_t* pos = p.h_meta + P;
+  uint32_t* outs = p.h_meta + 2 * P;
+  uint32_t* tab = p.h_meta + 2 * P + kMaxPrefillOutputs;
+  for (uint32_t i = 0; i < nrows; ++i) {
+    tok[i] = rows[i].token;
+    pos[i] = rows[i].position;
+    uint32_t* t = tab + (uint64_t)i * stride;
+    std::memcpy(t, rows[i].pages, rows[i].page_count * 4);
+    std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
+  }
+  for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
+  auto poison = [&](fh_status s2, const std::string& msg) {
+    ctx->poisoned = true;
+    return fail(ctx, s2, msg);
+  };
+  hipStream_t s = ctx->stream;
+  const uint32_t* d_tok = p.d_meta;
+  const uint32_t* d_pos = p.d_meta + P;
+  const uint32_t* d_out = p.d_meta + 2 * P;
+  const uint32_t* d_tab = p.d_meta + 2 * P + kMaxPrefillOutputs;
+  const uint64_t meta_bytes = (2ull * P + kMaxPrefillOutputs + (uint64_t)nrows * stride) * 4;
+  hipError_t e = hipMemcpyAsync(p.d_meta, p.h_meta, meta_bytes, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("metadata upload: ") + hipGetErrorString(e));
+  hipEventRecord(ctx->ev_begin, s);
+  if (ctx->profiling) ctx->prof_launches.clear();
+  Enq q{ctx};
+  (void)hipGetLastError();
+  uint32_t* err = ctx->err;
+  uint64_t n = 0;
+  auto L = [&](uint32_t cls, auto&& f) {
+    q.run(cls, f);
+    ++n;
+  };
+  const uint32_t R = nrows;
+  L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
+  L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, p.hidden, R, H, V, err, s); });
+  for (uint32_t l = 0; l < md.layers; ++l) {
+    const LayerWeights& W = ctx->layers[l];
+    uint16_t* kc = kv_cache(ctx, l, 0);
+    uint16_t* vc = kv_cache(ctx, l, 1);
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.in_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
+    });
+    L(FH_KC_QKV_GEMM, [&] {
+      return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, s);
+    });
+    L(FH_KC_QKNORM_ROPE_KV, [&] {
+      return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
+                                       p.qrot, kc, vc, R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
+    });
+    for (uint32_t r0 = 0; r0 < R; r0 += kPrefillAttnRows) {
+      const uint32_t rn = std::min(kPrefillAttnRows, R - r0);
+      L(FH_KC_ATTENTION, [&] {
+        return fh::launch_attention_partial(p.qrot + (uint64_t)r0 * Q, kc, vc, d_pos + r0,
+                                            d_tab + (uint64_t)r0 * stride, p.attn_part, p.attn, 1, r0, R, rn, QH, KVH,
+                                            stride, pages, C, err, s);
+      });
+      L(FH_KC_ATTENTION_MERGE, [&] {
+        return fh::launch_attention_merge(p.attn_part, d_pos + r0, p.attn, 1, r0, R, rn, QH, C, err, s);
+      });
+    }
+    L(FH_KC_O_GEMM, [&] {
+      return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);
+    });
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.post_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
+    });
+    L(FH_KC_GATE_UP_GEMM, [&] {
+      return fh::launch_gemm_large(p.xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, p.act, I, s);
+    });
+    L(FH_KC_DOWN_GEMM, [&] {
+      return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);
+    });
+  }
+  if (nout) {
+    L(FH_KC_RMSNORM, [&] { return fh::launch_gather_rows(p.hidden, d_out, p.out_hidden, nout, H, s); });
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(p.out_hidden, nullptr, 0, ctx->final_norm, p.out_xn, 1, nout, H,
+                                         md.rms_epsilon, err, s);
+    });
+    L(FH_KC_HEAD_GEMM, [&] {
+      return nout <= kMaxRows
+                 ? fh::launch_gemm(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, 1, nullptr, p.logits, V, s)
+                 : fh::launch_gemm_large(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, nullptr, p.logits, V, s);
+    });
+    L(FH_KC_ARGMAX, [&] { return fh::launch_argmax(p.logits, nout, V, p.argmax_scratch, p.choices, err, s); });
+    ++n;  // argmax is two launches
+  }
+  e = q.first_error;
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e));
+  hipEventRecord(ctx->ev_end, s);
+  if (nout) e = hipMemcpyAsync(p.h_out, p.choices, nout * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(p.h_out + kMaxPrefillOutputs, err, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("step: ") + hipGetErrorString(e));
+  hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);
+  if (ctx->profiling) collect_profile(ctx);
+  ctx->last_rows = nout;
+  ctx->last_logits = p.logits;
+  ctx->last_was_prefill = true;
+  const uint32_t errw = p.h_out[kMaxPrefillOutputs];
+  if (errw != 0) return poison(FH_ERR_NONFINITE, "device rejected the step:" + error_bits(errw));
+  for (uint32_t i = 0; i < nout; ++i) {
+    const uint32_t c = p.h_out[i];
+    if (c >= V) return poison(FH_ERR_NONFINITE, "batched GPU choice outside vocabulary");
+    choices_out[i] = c;
+  }
+  ctx->last_batch = batch_id;
+  ctx->dispatches += n;
+  return FH_OK;
+}
+
 fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
                            const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
   if (!ctx) return FH_ERR_INVALID_ARGUMENT;
   if (nout && (!output_rows || !choices_out)) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null output buffers");
   fh_status st = validate_batch(ctx, batch_id, rows, nrows, output_rows, nout);
   if (st != FH_OK) return st;
+  if (nrows > ctx->opt.row_capacity) return run_prefill(ctx, batch_id, rows, nrows, output_rows, nout, choices_out);
 
   const uint32_t cap = ctx->opt.row_capacity, stride = ctx->opt.page_table_stride;
   uint32_t* tok = ctx->h_meta;
@@ -790,19 +992,10 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("step: ") + hipGetErrorString(e));
   hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);
-  if (ctx->profiling) {
-    for (uint32_t c = 0; c < FH_KC_COUNT; ++c) {
-      ctx->class_ms[c] = 0.f;
-      ctx->class_launches[c] = 0;
-    }
-    for (const auto& pl : ctx->prof_launches) {
-      float ms = 0.f;
-      hipEventElapsedTime(&ms, pl.begin, pl.end);
-      ctx->class_ms[pl.cls] += ms;
-      ctx->class_launches[pl.cls] += 1;
-    }
-  }
+  if (ctx->profiling) collect_profile(ctx);
   ctx->last_rows = nrows;
+  ctx->last_logits = ctx->logits;
+  ctx->last_was_prefill = false;
   const uint32_t errw = ctx->h_out[cap];
   if (errw != 0) return poison(FH_ERR_NONFINITE, "device rejected the step:" + error_bits(errw));
   for (uint32_t i = 0; i < nout; ++i) {
@@ -818,12 +1011,12 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
 fh_status fh_read_logits(fh_ctx* ctx, float* out, uint64_t elements) {
   if (!ctx || !out || elements > (uint64_t)ctx->last_rows * ctx->md.vocabulary)
     return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad logits request");
-  FH_HIP(ctx, hipMemcpy(out, ctx->logits, elements * 4, hipMemcpyDeviceToHost));
+  FH_HIP(ctx, hipMemcpy(out, ctx->last_logits, elements * 4, hipMemcpyDeviceToHost));
   return FH_OK;
 }
 
 fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t elements) {
-  if (!ctx || !out || !ctx->capture || layer >= ctx->md.layers ||
+  if (!ctx || !out || !ctx->capture || ctx->last_was_prefill || layer >= ctx->md.layers ||
       elements > (uint64_t)ctx->last_rows * ctx->md.hidden)
     return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad hidden-state request (capture_hidden off?)");
   FH_HIP(ctx, hipMemcpy(out, ctx->capture + (uint64_t)layer * ctx->opt.row_capacity * ctx->md.hidden, elements * 2,
@@ -839,7 +1032,8 @@ fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled) {
   if (!ctx) return FH_ERR_INVALID_ARGUMENT;
   ctx->profiling = enabled != 0;
   if (ctx->profiling && ctx->prof_events.empty()) {
-    const uint64_t need = 2 * (8 + 12ull * ctx->md.layers);
+    const uint64_t attn_blocks = ctx->opt.prefill_rows ? (ctx->opt.prefill_rows + kPrefillAttnRows - 1) / kPrefillAttnRows : 1;
+    const uint64_t need = 2 * (12 + (10ull + 2 * attn_blocks) * ctx->md.layers);
     for (uint64_t i = 0; i < need; ++i) {
       hipEvent_t ev;
       FH_HIP(ctx, hipEventCreate(&ev));

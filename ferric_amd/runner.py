@@ -112,14 +112,14 @@ class TpBatchRunner:
     """One-GPU runner behind the reference's batch-runner boundary."""
 
     def __init__(self, model: dict, limits: PagedLimits, row_capacity: int = 32, use_graphs: bool = True,
-                 capture_hidden: bool = False, device: int = 0):
+                 capture_hidden: bool = False, device: int = 0, prefill_rows: int = 0):
         self._lib = load()
         self.model = dict(model)
         self.limits = limits
         self._desc = model_desc(model)
         self._opts = _lib.CtxOptions(row_capacity, limits.physical_page_count, limits.page_table_stride,
                                      limits.context_tokens, 1 if use_graphs else 0, 1 if capture_hidden else 0,
-                                     device)
+                                     device, prefill_rows)
         ctx = ctypes.c_void_p()
         st = self._lib.fh_create(ctypes.byref(self._desc), ctypes.byref(self._opts), ctypes.byref(ctx))
         check(st, None, "fh_create")
@@ -141,7 +141,8 @@ class TpBatchRunner:
                                         choices.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
         del keep
         check(st, self._ctx)
-        self._rows_last = len(batch.rows)
+        # Decode batches produce logits for every row, prefill chunks for the output rows only.
+        self._rows_last = len(batch.rows) if len(batch.rows) <= self._opts.row_capacity else len(outs)
         return BatchOutput([int(c) for c in choices[: len(outs)]])
 
     def output_head_rows(self, physical: int, published: int) -> int:

@@ -92,6 +92,7 @@ typedef struct fh_ctx_options {
   uint32_t use_graphs;        /* 1: replay one HIP graph per row count */
   uint32_t capture_hidden;    /* 1: keep every layer's residual output for fh_read_hidden */
   int32_t device;             /* HIP device ordinal */
+  uint32_t prefill_rows;      /* 0, or the largest batch (> row_capacity) run as a prefill chunk */
 } fh_ctx_options;
 
 /* One prepared row; mirrors EngineeringTpPreparedRowV1 (tp_paged.rs:257-300). */
@@ -143,6 +144,10 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
 
 /* Runs one forward step over the prepared rows and writes the greedy choice of
  * each requested output row (ascending row indices) to choices_out[nout].
+ * Up to row_capacity rows run the decode path (weight-streaming projections,
+ * one HIP graph per row count); larger batches, up to prefill_rows, run the
+ * prefill path (compute-bound MFMA projections; logits only for output rows;
+ * fh_read_logits then returns the output rows' logits in output order).
  * Replaces EngineeringTpBatchRunnerV2::execute_batch (tp_batch_runtime.rs:51-58)
  * / EngineeringTpBatchExecutionV2::forward (batched.rs:1746-2454). batch_id must
  * increase strictly (batched.rs:1700). On failure nothing is published and the
@@ -205,7 +210,9 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
 /* K1 projections: out = epilogue(x[m][k] . W[n][k]^T) with FP32 accumulation on MFMA.
  * epilogue: FH_EPI_BF16 (one RNE), FH_EPI_RESIDUAL (bf16((0 + acc) + residual), may alias out),
  * FH_EPI_SWIGLU (w from fh_op_tile_gate_up, n = 2*i, out [m][i] = swiglu(bf16(g), bf16(u))),
- * FH_EPI_F32 (FP32 out, the LM head). m <= 32. Replaces gemm.rs:161/:605 and
+ * FH_EPI_F32 (FP32 out, the LM head). m <= 32 streams the weight (decode, split-K allowed);
+ * m > 32 runs the compute-bound prefill kernel (n % 128 == 0, splits = 1, ldo % 4 == 0,
+ * no FH_EPI_PARTIAL). Replaces gemm.rs:161/:605 and
  * device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15/:142/:241, collective.rs:25,
  * activation.rs:32 and device/qwen3-tp-fp32-head32-kernels-v8/src/projection.rs:66/:186. */
 enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3, FH_EPI_PARTIAL = 4 };
@@ -218,14 +225,17 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
                      void* stream);
 /* Split-K factor the runtime uses for an n x k projection. */
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k);
-/* Row-major [m][k] bf16 <-> activation tile order (m <= 32; the tiled buffer holds 32 x k). */
+/* Rows a tiled activation buffer for m rows holds: 32 for m <= 32, else m rounded up to 128. */
+uint32_t fh_activation_rows(uint32_t m);
+/* Row-major [m][k] bf16 <-> activation tile order (the tiled buffer holds fh_activation_rows(m) x k). */
 fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream);
 fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t m, uint32_t k, void* stream);
 
 /* K2 residual + RMSNorm, fused: when splits > 0, hidden[r] = bf16((0 + sum_s partials[s][r]) +
  * hidden[r]) is written back first (the TP1 residual, v5 collective.rs:25-60, with the split-K
  * slabs summed in order), then y = RMSNorm(hidden) is written in activation tile order
- * (y_tiled = 1) or row-major. partials: `splits` slabs of [32][width] FP32. */
+ * (y_tiled = 1, fh_activation_rows(rows) rows) or row-major. partials: `splits` slabs of
+ * [32][width] FP32 (rows <= 32 when splits > 0). */
 fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* weight,
                                  uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float epsilon,
                                  uint32_t* error_word, void* stream);
@@ -246,7 +256,8 @@ fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint1
 
 /* K4 paged GQA decode attention: split-context partitions then an ordered merge.
  * q: [rows][qh*128]; out: [rows][qh*128] bf16 row-major, or activation tile order when
- * out_tiled (the output projection's input); scratch: fh_attention_scratch_bytes().
+ * out_tiled (the output projection's input, fh_activation_rows(rows) rows);
+ * scratch: fh_attention_scratch_bytes().
  * Replaces qwen3_paged_gqa_decode_bf16_f32_v1 (paged_decode.rs:222) and the split8
  * partial/merge pair (device/qwen3-tp-c1-split8-attention-kernels-v21/src/attention.rs:16, :214). */
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens);

@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 def test_struct_layouts_match_the_header():
     # Field counts and widths of the boundary structs.
     assert ctypes.sizeof(_lib.ModelDesc) == 10 * 4
-    assert ctypes.sizeof(_lib.CtxOptions) == 7 * 4
+    assert ctypes.sizeof(_lib.CtxOptions) == 8 * 4
     assert _lib.Row.pages.offset == 16 and ctypes.sizeof(_lib.Row) == 32
     from ferric_amd.runner import ROW_DTYPE
     assert ROW_DTYPE.itemsize == ctypes.sizeof(_lib.Row)
@@ -98,7 +98,9 @@ def test_ops_reject_bad_shapes_before_any_launch():
     lib = ferric_amd.load()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     assert lib.fh_op_gemm(p, p, 0, 64, 64, 0, 1, None, p, 64, None) == 1  # m = 0
-    assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None) == 1  # m > 32
+    assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None) == 1  # m > 32 needs n % 128
+    assert lib.fh_op_gemm(p, p, 33, 128, 64, 4, 1, None, p, 128, None) == 1  # m > 32: no split-K partials
+    assert lib.fh_op_gemm(p, p, 33, 128, 64, 0, 1, None, p, 130, None) == 1  # m > 32: 8-byte aligned rows
     assert lib.fh_op_gemm(p, p, 4, 60, 64, 0, 1, None, p, 64, None) == 1  # n % 16
     assert lib.fh_op_gemm(p, p, 4, 64, 48, 0, 1, None, p, 64, None) == 1  # k % 32
     assert lib.fh_op_gemm(p, p, 4, 64, 64, 1, 1, None, p, 64, None) == 1  # residual epilogue without residual
@@ -106,25 +108,26 @@ def test_ops_reject_bad_shapes_before_any_launch():
     assert lib.fh_op_gemm(p, p, 4, 64, 64, 0, 2, None, p, 64, None) == 1  # splits on a non-partial epilogue
     assert lib.fh_op_gemm(p, p, 4, 64, 64, 4, 3, None, p, 64, None) == 1  # more splits than k-blocks
     assert lib.fh_op_tile_weight(p, p, 17, 32, None) == 1
-    assert lib.fh_op_tile_activation(p, p, 33, 64, None) == 1
+    assert lib.fh_op_tile_activation(p, p, 33, 48, None) == 1  # k % 32
+    assert lib.fh_activation_rows(1) == 32 and lib.fh_activation_rows(32) == 32
+    assert lib.fh_activation_rows(33) == 128 and lib.fh_activation_rows(129) == 256
     assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1
     assert lib.fh_op_residual_rmsnorm(p, None, 2, p, p, 1, 4, 4096, 1e-6, None, None) == 1  # partials missing
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
-    assert lib.fh_op_paged_attention(p, p, p, p, p, p, 1, p, 40, 32, 8, 4, 4, 64, None, None) == 1  # tiled > 32 rows
 
 
 def test_create_rejects_unsupported_shapes_without_touching_the_device():
     lib = ferric_amd.load()
     desc = _lib.ModelDesc(2, 1024, 16, 8, 64, 3072, 151936, 1, 1_000_000, 1e-6)  # head_dim 64
-    opts = _lib.CtxOptions(8, 64, 32, 512, 0, 0, 0)
+    opts = _lib.CtxOptions(8, 64, 32, 512, 0, 0, 0, 0)
     ctx = ctypes.c_void_p()
     assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
     assert b"unsupported model shape" in lib.fh_last_error(None)
     desc = _lib.ModelDesc(2, 1024, 16, 8, 128, 3072, 151936, 1, 1_000_000, 1e-6)
-    opts = _lib.CtxOptions(33, 64, 32, 512, 0, 0, 0)  # more rows than the 32-row envelope
+    opts = _lib.CtxOptions(33, 64, 32, 512, 0, 0, 0, 0)  # more rows than the 32-row envelope
     assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
-    opts = _lib.CtxOptions(8, 64, 16, 512, 0, 0, 0)  # stride * 16 < context
+    opts = _lib.CtxOptions(8, 64, 16, 512, 0, 0, 0, 0)  # stride * 16 < context
     assert lib.fh_create(ctypes.byref(desc), ctypes.byref(opts), ctypes.byref(ctx)) == 1
 
 

@@ -120,26 +120,33 @@ def test_rmsnorm_known_answers():
         assert du.to_host(err, np.uint32)[0] != 0
 
 
+def tiled_rows(m):
+    """Rows of a tiled activation buffer: 32 up to 32 rows, else m rounded up to 128."""
+    return 32 if m <= 32 else -(-m // 128) * 128
+
+
 def act_tile_host(x, m, k):
-    """Numpy statement of the activation tile order for x[m][k] (m <= 32):
+    """Numpy statement of the activation tile order for x[m][k]:
     tile (kb, mt) = rows 16 mt.., cols 32 kb..; lane = row % 16 + 16 * ((col % 32) // 8)."""
-    full = np.zeros((32, k), np.uint16)
+    rows = tiled_rows(m)
+    full = np.zeros((rows, k), np.uint16)
     full[:m] = x.reshape(m, k)
-    t = full.reshape(2, 16, k // 32, 4, 8)  # mt, r, kb, g, e
+    t = full.reshape(rows // 16, 16, k // 32, 4, 8)  # mt, r, kb, g, e
     t = t.transpose(2, 0, 3, 1, 4)  # kb, mt, g, r, e -> lane = g*16 + r
     return np.ascontiguousarray(t).reshape(-1)
 
 
 def to_tiled_act(x, m, k):
     dx = du.to_dev(x)
-    dxt = du.empty(32 * k, np.uint16)
+    assert LIB.fh_activation_rows(m) == tiled_rows(m)
+    dxt = du.empty(tiled_rows(m) * k, np.uint16)
     _lib.check(LIB.fh_op_tile_activation(du.ptr(dx), du.ptr(dxt), m, k, du.stream()))
     return dxt
 
 
 def test_activation_tile_order_round_trip():
     r = rng(8)
-    for m, k in [(1, 32), (7, 64), (16, 1024), (17, 96), (32, 4096)]:
+    for m, k in [(1, 32), (7, 64), (16, 1024), (17, 96), (32, 4096), (33, 64), (130, 96), (300, 32)]:
         x = r.integers(0, 65536, m * k, dtype=np.uint64).astype(np.uint16)
         dxt = to_tiled_act(x, m, k)  # rows >= m stay zero (never written)
         assert np.array_equal(du.to_host(dxt, np.uint16), act_tile_host(x, m, k)), (m, k)
@@ -160,7 +167,7 @@ def _gemm_case(m, n, k, epi, seed, splits=1):
         gate, up = w[: i * k], w[i * k:]
         dg, du_ = du.to_dev(gate), du.to_dev(up)
         _lib.check(LIB.fh_op_tile_gate_up(du.ptr(dg), du.ptr(du_), du.ptr(dt), i, k, du.stream()))
-        out_t = du.empty(32 * i, np.uint16)  # activation tile order (the down projection's input)
+        out_t = du.empty(tiled_rows(m) * i, np.uint16)  # activation tile order (the down projection's input)
         _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out_t), i, du.stream()))
         out = du.empty(m * i, np.uint16)
         _lib.check(LIB.fh_op_untile_activation(du.ptr(out_t), du.ptr(out), m, i, du.stream()))
@@ -226,15 +233,39 @@ def test_gemm_residual_and_swiglu_epilogues(m):
         assert np.mean(got == ref) > 0.97
 
 
+@pytest.mark.parametrize("m", [33, 130, 257])
+@pytest.mark.parametrize("n,k", [(128, 64), (256, 1024), (384, 4096)])
+def test_gemm_large_m_bf16_and_f32_epilogues(m, n, k):
+    # Prefill-size batches take the compute-bound kernel (128 x 128 blocks, no split-K).
+    got, ref = _gemm_case(m, n, k, _lib.EPI_F32, m * 5 + n)
+    assert np.max(np.abs(got - ref)) <= F32_BOUND
+    got, ref = _gemm_case(m, n, k, _lib.EPI_BF16, m * 5 + n + 1)
+    assert du.bf16_close(got, ref, ulps=1)
+    assert np.mean(got == ref) > 0.99
+
+
+@pytest.mark.parametrize("m", [40, 200])
+def test_gemm_large_m_residual_and_swiglu_epilogues(m):
+    got, ref = _gemm_case(m, 512, 4096, _lib.EPI_RESIDUAL, 77 + m)
+    assert du.bf16_close(got, ref, ulps=1)
+    assert np.mean(got == ref) > 0.99
+    for n in (256, 1024):
+        got, ref = _gemm_case(m, n, 1024, _lib.EPI_SWIGLU, 177 + m + n)
+        assert du.bf16_close(got, ref, ulps=3)
+        assert np.mean(got == ref) > 0.97
+
+
 @pytest.mark.parametrize("splits", [0, 1, 3])
-@pytest.mark.parametrize("rows,width", [(1, 1024), (32, 4096), (9, 4096)])
+@pytest.mark.parametrize("rows,width", [(1, 1024), (32, 4096), (9, 4096), (100, 1024)])
 def test_residual_rmsnorm(splits, rows, width):
+    if splits and rows > 32:
+        pytest.skip("split-K partial slabs hold 32 rows")
     r = rng(splits * 100 + rows)
     hidden = rand_bf16(r, rows * width, 2.0)
     w = rand_bf16(r, width, 1.0)
     slabs = (r.standard_normal((max(splits, 1), 32, width)) * 0.5).astype(np.float32)
     dh, dw_, dp = du.to_dev(hidden), du.to_dev(w), du.to_dev(slabs.reshape(-1))
-    dy = du.empty(32 * width, np.uint16)
+    dy = du.empty(tiled_rows(rows) * width, np.uint16)
     err = du.empty(1, np.uint32)
     _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp) if splits else None, splits, du.ptr(dw_), du.ptr(dy),
                                           1, rows, width, 1e-6, du.ptr(err), du.stream()))
@@ -330,18 +361,22 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh, splits):
 
 
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
-@pytest.mark.parametrize("tiled", [0, 1])
-def test_paged_attention_within_tolerance(qh, kvh, tiled):
-    r = rng(1000 + qh)
+@pytest.mark.parametrize("tiled,many", [(0, False), (1, False), (1, True)])
+def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
+    r = rng(1000 + qh + 7 * many)
     pages, stride, context = 600, 520, 8320
-    # one partition (<= 512 tokens), several partitions, page-boundary and partial-page cases
-    positions = np.array([0, 15, 16, 255, 511, 512, 513, 1000, 4095, 8319, 77, 8190, 6000], np.uint32)
+    if many:
+        # a prefill-size batch: 40 rows, tiled output of fh_activation_rows(40) rows
+        positions = r.integers(0, 2000, 40).astype(np.uint32)
+    else:
+        # one partition (<= 256 tokens), several partitions, page-boundary and partial-page cases
+        positions = np.array([0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 8319, 77, 8190, 6000], np.uint32)
     rows = len(positions)
     kc, vc = _paged_pool(r, pages, kvh)
     q = rand_bf16(r, rows * qh * 128, 1.0)
     table = np.stack([r.permutation(pages)[:stride] for _ in range(rows)]).astype(np.uint32)
     scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
-    out = du.empty((32 if tiled else rows) * qh * 128, np.uint16)
+    out = du.empty((tiled_rows(rows) if tiled else rows) * qh * 128, np.uint16)
     err = du.empty(1, np.uint32)
     dkc, dvc = du.to_dev(kc), du.to_dev(vc)
     dq, dpos, dtab = du.to_dev(q), du.to_dev(positions), du.to_dev(table)

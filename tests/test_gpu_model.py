@@ -44,9 +44,10 @@ def tables_of(batch, stride):
 class Pair:
     """A GPU runner and the CPU oracle model with identical contents."""
 
-    def __init__(self, cfg, limits, seed=7, capture=True, graphs=False, rows=32):
+    def __init__(self, cfg, limits, seed=7, capture=True, graphs=False, rows=32, prefill_rows=0):
         self.cfg, self.limits = cfg, limits
-        self.gpu = TpBatchRunner(cfg, limits, row_capacity=rows, use_graphs=graphs, capture_hidden=capture)
+        self.gpu = TpBatchRunner(cfg, limits, row_capacity=rows, use_graphs=graphs, capture_hidden=capture,
+                                 prefill_rows=prefill_rows)
         self.gpu.synthesize_weights(seed, 0.02)
         self.cpu = orc.Model(cfg, limits.physical_page_count)
         self.cpu.synthesize(seed, 0.02)
@@ -70,14 +71,19 @@ class Pair:
                              self.limits.context_tokens)
         return sids
 
-    def step(self, rows):
+    def step(self, rows, outs=None):
+        """One step; `outs` selects the output rows (default: every row). The
+        oracle's logits, choices and gaps are narrowed to the same rows."""
         batch = self.pool.prepare(rows)
-        out = self.gpu.execute_batch(batch, list(range(len(rows))))
+        outs = list(range(len(rows))) if outs is None else list(outs)
+        out = self.gpu.execute_batch(batch, outs)
         stride = self.limits.page_table_stride
         t, c = tables_of(batch, stride)
         ref = self.cpu.forward([r.token for r in batch.rows], [r.position for r in batch.rows], t, c, stride,
                                want_logits=True, want_hidden=True)
         ref["tables"], ref["counts"] = t, c
+        for key in ("logits", "choices", "gaps"):
+            ref[key] = ref[key][outs]
         self.pool.commit(batch)
         return batch, out, ref
 
@@ -304,3 +310,50 @@ def test_full_small_model_prompt_then_greedy_decode():
         pair.check_kv(layer_list=[0, 27])
     finally:
         pair.close()
+
+
+def _prefill_case(cfg, limits, prompts, decode_lengths, prefill_rows, seed, label):
+    """Prompts (from position 0) plus decode rows of sequences with a KV
+    prefix, as one batch larger than row_capacity: the prefill path. The
+    output rows are each prompt's last token and every decode row."""
+    pair = Pair(cfg, limits, seed=seed, capture=False, rows=8, prefill_rows=prefill_rows)
+    try:
+        rng = np.random.default_rng(seed)
+        dec = pair.admit_with_prefix(decode_lengths) if decode_lengths else []
+        rows, outs = [], []
+        for n in prompts:
+            sid = pair.pool.admit(0)
+            rows += [(sid, int(t)) for t in rng.integers(0, cfg["vocabulary"], n)]
+            outs.append(len(rows) - 1)
+        for sid in dec:
+            rows.append((sid, int(rng.integers(0, cfg["vocabulary"]))))
+            outs.append(len(rows) - 1)
+        assert len(rows) > 8
+        batch, out, ref = pair.step(rows, outs)
+        _mark_written(pair, batch)
+        pair.check(batch, out, ref, label)
+        pair.check_kv()
+        # the next step decodes every sequence through the 8-row decode path
+        seqs = sorted({r.sequence for r in batch.rows})[:8]
+        last = {r.sequence: i for i, r in enumerate(batch.rows)}
+        toks = {s: int(out.choices[outs.index(last[s])]) for s in seqs}
+        batch, out, ref = pair.step([(s, toks[s]) for s in seqs])
+        _mark_written(pair, batch)
+        pair.check(batch, out, ref, label + " then decode")
+    finally:
+        pair.close()
+
+
+def test_prefill_chunk_matches_oracle():
+    # 0.6B shape, 2 layers: 280 rows (two 130-token prompts + 20 decode rows),
+    # two attention row blocks and a padded 384-row tile buffer.
+    cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
+    limits = PagedLimits(context_tokens=2048, physical_page_count=800, page_table_stride=128)
+    _prefill_case(cfg, limits, [130, 130], [5, 16, 17, 600, 1500] * 4, 512, 31, "prefill 0.6b")
+
+
+def test_prefill_chunk_8b_layer_shapes():
+    # 8B layer geometry, one layer: a 40-row prompt beside two decode rows.
+    cfg = dict(ferric_amd.QWEN3_8B, layers=1)
+    limits = PagedLimits(context_tokens=4096, physical_page_count=300, page_table_stride=256)
+    _prefill_case(cfg, limits, [40], [100, 3000], 64, 37, "prefill 8b")
