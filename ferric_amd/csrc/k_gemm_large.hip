@@ -1,14 +1,16 @@
 // K1 projections for prefill and wide verify batches (m > 32 token rows):
 // bf16 MFMA (v_mfma_f32_16x16x32_bf16), FP32 accumulation, compute-bound.
 //
-// Operands come straight from their tile orders (common.hpp): the weight in
-// weight tile order and the activation in activation tile order with
-// act_mtiles(m) row tiles, so every operand load of a wave is one contiguous
-// 1 KiB that lands in MFMA registers. A workgroup of 4 waves computes a
-// 128 (n) x 128 (m) block: waves 0/1 and 2/3 share m rows, waves 0/2 and 1/3
-// share n rows, so each operand tile is fetched by two waves of the block
-// (the second fetch hits the CU's cache). Each wave accumulates 4 x 4 MFMA
-// tiles over the whole k range, with the next k-block's operands in flight.
+// Operands come from their tile orders (common.hpp): the weight in weight
+// tile order and the activation in activation tile order with act_mtiles(m)
+// row tiles, so every operand fetch of a wave is one contiguous 1 KiB in the
+// exact MFMA register layout. Two kernels:
+//  * gemm_large_lds_kernel (n % 256 == 0: every projection): 256 x 256
+//    blocks of 8 waves sharing each k-block's operand tiles through LDS;
+//  * gemm_large_kernel (the LM head's 151936 rows): 128 x 128 blocks of 4
+//    waves loading operands straight into registers (each tile fetched by
+//    two waves; the second fetch hits the CU's cache).
+// Each wave accumulates its MFMA tiles over the whole k range.
 //
 // Epilogues (same rounding points as the decode kernel, no split-K here):
 //   FH_EPI_BF16     out[m][n] = bf16(acc)
@@ -29,7 +31,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kNT = 4;  // n-tiles per wave
 constexpr int kMT = 4;  // m-tiles per wave
 constexpr int kBlockTiles = 2 * kNT;  // 16-row tiles per block side (128 rows)
-static_assert(kLargeBlockRows == 16 * 2 * kMT, "block rows match the wave layout");
+static_assert(kLargeBlockRows % (16 * 2 * kMT) == 0, "padded rows cover whole blocks");
 
 __device__ __forceinline__ bf16x8 b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -134,6 +136,139 @@ __global__ __launch_bounds__(256) void gemm_large_kernel(const uint16_t* __restr
   }
 }
 
+// 256 x 256 blocks for weights with n % 256 == 0 (every projection): 8 waves,
+// each 8 n-tiles x 4 m-tiles (wave grid 2 along n x 4 along m). Per 32-wide
+// k-block the block's 16 weight tiles and 16 activation tiles are fetched
+// once (waves 0-3: weight tiles, waves 4-7: activation tiles, one 16-byte
+// load per lane per tile) and shared through LDS; the next two k-blocks'
+// fetches are in flight in registers while the current one is computed.
+constexpr int kBigTiles = 16;  // 16-row tiles per block side (256 rows)
+#ifndef FH_BIG_WAVES_N
+#define FH_BIG_WAVES_N 2
+#define FH_BIG_WAVES_M 4
+#endif
+constexpr int kBigWavesN = FH_BIG_WAVES_N, kBigWavesM = FH_BIG_WAVES_M;
+static_assert(kLargeBlockRows % (16 * kBigTiles) == 0 || (16 * kBigTiles) % kLargeBlockRows == 0, "");
+
+template <int EPI, int WAVES_N, int WAVES_M>
+__global__ __launch_bounds__(WAVES_N * WAVES_M * 64) void gemm_large_lds_kernel(
+    const uint16_t* __restrict__ xt, const uint16_t* __restrict__ w, uint32_t m, uint32_t mtiles, uint32_t kb_count,
+    const uint16_t* residual, void* out, uint32_t ldo, uint32_t out_mtiles) {
+  constexpr int WAVES = WAVES_N * WAVES_M;
+  constexpr int WN = kBigTiles / WAVES_N, WM = kBigTiles / WAVES_M;  // tiles per wave
+  constexpr int FT = 2 * kBigTiles / WAVES;  // tiles each wave fetches per k-block
+  static_assert(kBigTiles % FT == 0, "a wave fetches weight tiles or activation tiles, not both");
+  __shared__ u32x4 lds[2][2 * kBigTiles][64];  // [stage][16 weight tiles | 16 activation tiles][lane]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t bn = blockIdx.x * kBigTiles, bm = blockIdx.y * kBigTiles;  // first tiles of the block
+
+  // Fetch role: the first half of the waves fetch weight tiles, the second
+  // half activation tiles, FT consecutive tiles each.
+  const bool fetch_w = wave < WAVES / 2;
+  const uint32_t f0 = (fetch_w ? wave : wave - WAVES / 2) * FT;
+  const u32x4* gsrc = fetch_w ? reinterpret_cast<const u32x4*>(w) + (uint64_t)(bn + f0) * kb_count * 64 + lane
+                              : reinterpret_cast<const u32x4*>(xt) + (uint64_t)(bm + f0) * 64 + lane;
+  const uint64_t g_tile_stride = fetch_w ? (uint64_t)kb_count * 64 : 64;  // next tile
+  const uint64_t g_kb_stride = fetch_w ? 64 : (uint64_t)mtiles * 64;      // next k-block
+  const int slot0 = (fetch_w ? 0 : kBigTiles) + f0;
+
+  u32x4 ga[FT], gb[FT];
+  auto fetch = [&](u32x4(&g)[FT], uint32_t kb) {
+#pragma unroll
+    for (int t = 0; t < FT; ++t) g[t] = gsrc[t * g_tile_stride + kb * g_kb_stride];
+  };
+  auto stash = [&](const u32x4(&g)[FT], int stage) {
+#pragma unroll
+    for (int t = 0; t < FT; ++t) lds[stage][slot0 + t][lane] = g[t];
+  };
+
+  const int wn = wave % WAVES_N, wm = wave / WAVES_N;  // compute role
+  f32x4 acc[WN][WM];
+#pragma unroll
+  for (int i = 0; i < WN; ++i)
+#pragma unroll
+    for (int j = 0; j < WM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int stage) {
+    u32x4 wv[WN], xv[WM];
+#pragma unroll
+    for (int i = 0; i < WN; ++i) wv[i] = lds[stage][wn * WN + i][lane];
+#pragma unroll
+    for (int j = 0; j < WM; ++j) xv[j] = lds[stage][kBigTiles + wm * WM + j][lane];
+#pragma unroll
+    for (int i = 0; i < WN; ++i)
+#pragma unroll
+      for (int j = 0; j < WM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(wv[i]), b8(xv[j]), acc[i][j], 0, 0, 0);
+  };
+
+  // Prologue: k-block 0 into LDS stage 0, k-block 1 in flight.
+  fetch(ga, 0);
+  if (kb_count > 1) fetch(gb, 1);
+  stash(ga, 0);
+  __syncthreads();
+  // Iteration kb computes stage kb % 2 while k-block kb + 1 (already in
+  // registers) goes to the other stage and k-block kb + 2 is fetched.
+  for (uint32_t kb = 0; kb < kb_count; kb += 2) {
+    if (kb + 2 < kb_count) fetch(ga, kb + 2);
+    compute(0);
+    if (kb + 1 < kb_count) stash(gb, 1);
+    __syncthreads();
+    if (kb + 1 < kb_count) {
+      if (kb + 3 < kb_count) fetch(gb, kb + 3);
+      compute(1);
+      if (kb + 2 < kb_count) stash(ga, 0);
+      __syncthreads();
+    }
+  }
+
+  const uint32_t nt0 = bn + wn * WN, mt0 = bm + wm * WM;
+  if (mt0 * 16 >= m) return;  // this wave's rows are all padding
+  const uint32_t q = lane >> 4, c = lane & 15;
+  if constexpr (EPI == FH_EPI_SWIGLU) {
+    bool bad = false;
+#pragma unroll
+    for (int p = 0; p < WN / 2; ++p) {
+      const uint32_t col = ((nt0 + 2 * p) / 2) * 16 + 4 * q;
+#pragma unroll
+      for (int j = 0; j < WM; ++j) {
+        const uint32_t row = (mt0 + j) * 16 + c;
+        if (row >= m) continue;
+        uint32_t y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = swiglu_bf16(round_bf16(acc[2 * p][j][e]), round_bf16(acc[2 * p + 1][j][e]), bad);
+        uint2 v = make_uint2(y[0] | (y[1] << 16), y[2] | (y[3] << 16));
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + act_offset_m(row, col, out_mtiles)) = v;
+      }
+    }
+    (void)bad;
+  } else {
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      const uint32_t n = (nt0 + i) * 16 + 4 * q;
+#pragma unroll
+      for (int j = 0; j < WM; ++j) {
+        const uint32_t row = (mt0 + j) * 16 + c;
+        if (row >= m) continue;
+        const uint64_t o = (uint64_t)row * ldo + n;
+        if constexpr (EPI == FH_EPI_F32) {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + o) = acc[i][j];
+        } else if constexpr (EPI == FH_EPI_BF16) {
+          uint2 v = make_uint2(f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16),
+                               f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16));
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = v;
+        } else {
+          const uint2 rv = *reinterpret_cast<const uint2*>(residual + o);
+          const float r0 = lo_bf16(rv.x), r1 = hi_bf16(rv.x), r2 = lo_bf16(rv.y), r3 = hi_bf16(rv.y);
+          uint2 v = make_uint2(f32_to_bf16((0.0f + acc[i][j][0]) + r0) | (f32_to_bf16((0.0f + acc[i][j][1]) + r1) << 16),
+                               f32_to_bf16((0.0f + acc[i][j][2]) + r2) | (f32_to_bf16((0.0f + acc[i][j][3]) + r3) << 16));
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = v;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
@@ -141,8 +276,23 @@ hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, u
   if (n % (16 * kBlockTiles) != 0 || k % 32 != 0 || m == 0) return hipErrorInvalidValue;
   const uint32_t mtiles = act_mtiles(m);
   const uint32_t out_mtiles = epilogue == FH_EPI_SWIGLU ? act_mtiles(m) : 0u;
-  const dim3 grid(n / (16 * kBlockTiles), mtiles / kBlockTiles);
   const uint32_t kb = k / 32;
+  if (n % (16 * kBigTiles) == 0 && mtiles % kBigTiles == 0) {
+    const dim3 grid(n / (16 * kBigTiles), mtiles / kBigTiles);
+#define FH_BIG(E)                                                                                             \
+  hipLaunchKernelGGL((gemm_large_lds_kernel<E, kBigWavesN, kBigWavesM>), grid, dim3(64 * kBigWavesN * kBigWavesM), \
+                     0, s, x_tiled, w_tiled, m, mtiles, kb, residual, out, ldo, out_mtiles)
+    switch (epilogue) {
+      case FH_EPI_BF16: FH_BIG(FH_EPI_BF16); break;
+      case FH_EPI_RESIDUAL: FH_BIG(FH_EPI_RESIDUAL); break;
+      case FH_EPI_SWIGLU: FH_BIG(FH_EPI_SWIGLU); break;
+      case FH_EPI_F32: FH_BIG(FH_EPI_F32); break;
+      default: return hipErrorInvalidValue;
+    }
+#undef FH_BIG
+    return hipGetLastError();
+  }
+  const dim3 grid(n / (16 * kBlockTiles), mtiles / kBlockTiles);
   switch (epilogue) {
     case FH_EPI_BF16:
       hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_BF16>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,

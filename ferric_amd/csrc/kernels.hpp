@@ -22,9 +22,9 @@ constexpr uint32_t kArgmaxShards = 64;
 // split-K partial slabs are [kMaxRows][n] FP32.
 constexpr uint32_t kMaxRows = 32;
 // Prefill / wide batches (m > kMaxRows rows) run the large GEMM, whose
-// workgroups cover 128 activation rows; their activation buffers hold
+// workgroups cover 256 activation rows; their activation buffers hold
 // act_mtiles(m) 16-row tiles (decode buffers: 2).
-constexpr uint32_t kLargeBlockRows = 128;
+constexpr uint32_t kLargeBlockRows = 256;
 inline uint32_t act_mtiles(uint32_t m) {
   return m <= kMaxRows ? 2u : ((m + kLargeBlockRows - 1) / kLargeBlockRows) * (kLargeBlockRows / 16);
 }

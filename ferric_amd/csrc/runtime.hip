@@ -830,6 +830,9 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
   }
   for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
+  std::vector<uint32_t> block_max_pos((nrows + kPrefillAttnRows - 1) / kPrefillAttnRows, 0);
+  for (uint32_t i = 0; i < nrows; ++i)
+    block_max_pos[i / kPrefillAttnRows] = std::max(block_max_pos[i / kPrefillAttnRows], rows[i].position);
   auto poison = [&](fh_status s2, const std::string& msg) {
     ctx->poisoned = true;
     return fail(ctx, s2, msg);
@@ -876,9 +879,11 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
                                             d_tab + (uint64_t)r0 * stride, p.attn_part, p.attn, 1, r0, R, rn, QH, KVH,
                                             stride, pages, C, err, s);
       });
-      L(FH_KC_ATTENTION_MERGE, [&] {
-        return fh::launch_attention_merge(p.attn_part, d_pos + r0, p.attn, 1, r0, R, rn, QH, C, err, s);
-      });
+      // Rows whose context fits one partition finish in the partition kernel.
+      if (block_max_pos[r0 / kPrefillAttnRows] >= fh::kAttnSplitTokens)
+        L(FH_KC_ATTENTION_MERGE, [&] {
+          return fh::launch_attention_merge(p.attn_part, d_pos + r0, p.attn, 1, r0, R, rn, QH, C, err, s);
+        });
     }
     L(FH_KC_O_GEMM, [&] {
       return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);

@@ -211,7 +211,8 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
  * epilogue: FH_EPI_BF16 (one RNE), FH_EPI_RESIDUAL (bf16((0 + acc) + residual), may alias out),
  * FH_EPI_SWIGLU (w from fh_op_tile_gate_up, n = 2*i, out [m][i] = swiglu(bf16(g), bf16(u))),
  * FH_EPI_F32 (FP32 out, the LM head). m <= 32 streams the weight (decode, split-K allowed);
- * m > 32 runs the compute-bound prefill kernel (n % 128 == 0, splits = 1, ldo % 4 == 0,
+ * m > 32 runs the compute-bound prefill kernel (256 x 256 blocks through LDS when
+ * n % 256 == 0, else 128 x 128 blocks; n % 128 == 0, splits = 1, ldo % 4 == 0,
  * no FH_EPI_PARTIAL). Replaces gemm.rs:161/:605 and
  * device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15/:142/:241, collective.rs:25,
  * activation.rs:32 and device/qwen3-tp-fp32-head32-kernels-v8/src/projection.rs:66/:186. */
@@ -225,7 +226,7 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
                      void* stream);
 /* Split-K factor the runtime uses for an n x k projection. */
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k);
-/* Rows a tiled activation buffer for m rows holds: 32 for m <= 32, else m rounded up to 128. */
+/* Rows a tiled activation buffer for m rows holds: 32 for m <= 32, else m rounded up to 256. */
 uint32_t fh_activation_rows(uint32_t m);
 /* Row-major [m][k] bf16 <-> activation tile order (the tiled buffer holds fh_activation_rows(m) x k). */
 fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream);

@@ -121,8 +121,8 @@ def test_rmsnorm_known_answers():
 
 
 def tiled_rows(m):
-    """Rows of a tiled activation buffer: 32 up to 32 rows, else m rounded up to 128."""
-    return 32 if m <= 32 else -(-m // 128) * 128
+    """Rows of a tiled activation buffer: 32 up to 32 rows, else m rounded up to 256."""
+    return 32 if m <= 32 else -(-m // 256) * 256
 
 
 def act_tile_host(x, m, k):
