@@ -48,6 +48,10 @@ PREFILL_WORKLOADS = {
     "qwen3-8b-prefill": ("8b", 32, 256, "Qwen3-8B shape, one chunked-prefill batch of 32 prompts x 256 random ids "
                                         "from position 0 into a shuffled 16-token page pool; greedy first token"),
 }
+SPEC_WORKLOADS = {
+    "qwen3-8b-speculative": (32, 256, 4, "Qwen3-8B target + Qwen3-0.6B draft (random init), 32 prompts x 256 "
+                                         "random ids prefilled into both, then greedy speculative rounds with K=4"),
+}
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 
@@ -56,7 +60,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=64)
     p.add_argument("--warmup", type=int, default=4)
-    p.add_argument("--workload", default="qwen3-8b-b32", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS))
+    p.add_argument("--workload", default="qwen3-8b-b32",
+                   choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(SPEC_WORKLOADS))
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=2, help="decode steps the CPU oracle sample runs")
@@ -250,6 +255,59 @@ def prefill_bench(args, name):
     print(json.dumps(result), flush=True)
 
 
+def speculative_bench(args, name):
+    import torch
+
+    import ferric_amd
+    from ferric_amd import PagedLimits, PagePool, TpBatchRunner
+    from ferric_amd.speculative import SpeculativeDecoder
+
+    seqs, tokens, k, desc = SPEC_WORKLOADS[name]
+    rounds = max(1, args.steps)
+    context_tokens = (tokens + (rounds + args.warmup + 2) * (k + 1) + 15) // 16 * 16
+    stride = context_tokens // 16
+    limits = PagedLimits(context_tokens=context_tokens, physical_page_count=seqs * stride + 64,
+                         page_table_stride=stride)
+    target = TpBatchRunner(ferric_amd.QWEN3_8B, limits, row_capacity=32, use_graphs=True, prefill_rows=seqs * tokens)
+    draft = TpBatchRunner(ferric_amd.QWEN3_0_6B, limits, row_capacity=32, use_graphs=True,
+                          prefill_rows=seqs * tokens)
+    target.synthesize_weights(args.seed, 0.02)
+    draft.synthesize_weights(args.seed + 1, 0.02)
+    dec = SpeculativeDecoder(target, PagePool(limits, seed=args.seed), draft, PagePool(limits, seed=args.seed + 1), k=k)
+    rng = np.random.default_rng(args.seed)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.prefill([list(rng.integers(0, ferric_amd.QWEN3_8B["vocabulary"], tokens)) for _ in range(seqs)])
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        dec.round()
+    emitted = accepted = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(rounds):
+        st = dec.round()
+        emitted += sum(len(e) for e in st.emitted)
+        accepted += sum(st.accepted)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    result = {
+        "metric": f"speculative decode tokens/s, {desc}",
+        "value": round(emitted / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": rounds, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / rounds, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": desc, "sequences": seqs, "prompt_tokens": tokens, "k": k,
+                   "prefill_both_models_s": round(prefill_s, 3),
+                   "acceptance": round(accepted / (rounds * seqs * k), 4),
+                   "emitted_per_round": round(emitted / rounds, 2)},
+    }
+    target.close()
+    draft.close()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -262,6 +320,9 @@ def main():
 
     if args.workload in PREFILL_WORKLOADS:
         prefill_bench(args, args.workload)
+        return
+    if args.workload in SPEC_WORKLOADS:
+        speculative_bench(args, args.workload)
         return
 
     import torch

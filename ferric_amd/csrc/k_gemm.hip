@@ -38,10 +38,13 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// blockIdx.z selects a 32-row chunk of the activation (rows 32 z ..), for
+// batches of more than 32 rows: every chunk streams the same weight tiles,
+// which the chip's caches serve to the chunks' concurrent workgroups.
 template <int NT, int MT, int EPI, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __restrict__ xt,
-                                                         const uint16_t* __restrict__ w, uint32_t m,
-                                                         uint32_t kb_count, uint32_t kb_split,
+                                                         const uint16_t* __restrict__ w, uint32_t m_total,
+                                                         uint32_t kb_count, uint32_t kb_split, uint32_t x_mtiles,
                                                          const uint16_t* residual, void* out, uint32_t ldo) {
   __shared__ float red[WAVES][NT * MT * 256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -57,7 +60,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     wp[nt] = reinterpret_cast<const u32x4*>(w) + ((uint64_t)(tile0 + nt) * kb_count + kb_lo) * 64 + lane;
-  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)kb_lo * 128 + lane;
+  const uint32_t row0 = blockIdx.z * 32;
+  const uint32_t m = min(m_total - row0, 32u);
+  const uint64_t xkb = (uint64_t)x_mtiles * 64;  // 16-byte units per k-block of the activation
+  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)kb_lo * xkb + blockIdx.z * 128 + lane;
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)(s0 + u) * 64);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)(s0 + u) * 128 + mt * 64];
+      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)(s0 + u) * xkb + mt * 64];
     }
   };
   auto compute = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT]) {
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) wv[nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)s * 64);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[(uint64_t)s * 128 + mt * 64];
+    for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[(uint64_t)s * xkb + mt * 64];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -147,7 +153,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
       if (row < m) {
         const uint32_t col = (tile0 / 2 + pair) * 16 + i;
         const uint32_t y = swiglu_bf16(round_bf16(g), round_bf16(u), bad);
-        reinterpret_cast<uint16_t*>(out)[act_offset(row, col)] = (uint16_t)y;
+        reinterpret_cast<uint16_t*>(out)[act_offset_m(row0 + row, col, act_mtiles(m_total))] = (uint16_t)y;
       }
     }
     (void)bad;  // a nonfinite activation surfaces at the next residual + norm
@@ -161,7 +167,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
       for (int wv = 1; wv < WAVES; ++wv) v += red[wv][idx];
       if (row >= m) continue;
       const uint64_t n = (uint64_t)(tile0 + nt) * 16 + i;
-      const uint64_t o = (uint64_t)row * ldo + n;
+      const uint64_t o = (uint64_t)(row0 + row) * ldo + n;
       if constexpr (EPI == FH_EPI_PARTIAL) {
         reinterpret_cast<float*>(out)[(uint64_t)split * kMaxRows * ldo + o] = v;
       } else if constexpr (EPI == FH_EPI_BF16) {
@@ -181,13 +187,15 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
                     const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
   const uint32_t kb = k / 32;
   const uint32_t kb_split = (kb + splits - 1) / splits;
-  dim3 grid(n / (16 * NT), splits);
+  const uint32_t chunks = (m + 31) / 32;
+  dim3 grid(n / (16 * NT), splits, chunks);
+  const uint32_t x_mtiles = act_mtiles(m);
   if (m <= 16)
     hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       residual, out, ldo);
+                       x_mtiles, residual, out, ldo);
   else
     hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       residual, out, ldo);
+                       x_mtiles, residual, out, ldo);
 }
 
 // Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections):
@@ -229,7 +237,7 @@ uint32_t gemm_default_splits(uint32_t n, uint32_t k) { return choose_splits(n, k
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        hipStream_t s) {
-  if (splits == 0) return hipErrorInvalidValue;
+  if (splits == 0 || (m > kMaxRows && (splits != 1 || epilogue == FH_EPI_PARTIAL))) return hipErrorInvalidValue;
   switch (epilogue) {
     case FH_EPI_BF16: launch_epi<FH_EPI_BF16>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
     case FH_EPI_RESIDUAL: launch_epi<FH_EPI_RESIDUAL>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;

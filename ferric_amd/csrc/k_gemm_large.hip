@@ -28,6 +28,7 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr uint32_t kStreamedRows = 256;
 constexpr int kNT = 4;  // n-tiles per wave
 constexpr int kMT = 4;  // m-tiles per wave
 constexpr int kBlockTiles = 2 * kNT;  // 16-row tiles per block side (128 rows)
@@ -273,7 +274,11 @@ __global__ __launch_bounds__(WAVES_N * WAVES_M * 64) void gemm_large_lds_kernel(
 
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                              uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
-  if (n % (16 * kBlockTiles) != 0 || k % 32 != 0 || m == 0) return hipErrorInvalidValue;
+  // Up to kStreamedRows rows the weight-streaming kernel is faster: it runs
+  // 32-row chunks of the batch against the same weight tiles (a prefill
+  // chunk of 17..32 rows when row_capacity < 32, a speculative verify batch).
+  if (m <= kStreamedRows) return launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, 1, residual, out, ldo, s);
+  if (n % (16 * kBlockTiles) != 0 || k % 32 != 0) return hipErrorInvalidValue;
   const uint32_t mtiles = act_mtiles(m);
   const uint32_t out_mtiles = epilogue == FH_EPI_SWIGLU ? act_mtiles(m) : 0u;
   const uint32_t kb = k / 32;

@@ -25,7 +25,7 @@ constexpr uint32_t kMaxRows = 32;
 // workgroups cover 256 activation rows; their activation buffers hold
 // act_mtiles(m) 16-row tiles (decode buffers: 2).
 constexpr uint32_t kLargeBlockRows = 256;
-inline uint32_t act_mtiles(uint32_t m) {
+__host__ __device__ inline uint32_t act_mtiles(uint32_t m) {
   return m <= kMaxRows ? 2u : ((m + kLargeBlockRows - 1) / kLargeBlockRows) * (kLargeBlockRows / 16);
 }
 

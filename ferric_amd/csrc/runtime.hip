@@ -111,6 +111,7 @@ struct fh_ctx {
   } pre;
   const float* last_logits = nullptr;  // what fh_read_logits copies
   bool last_was_prefill = false;
+  std::string launch_detail;  // which launch failed first in the last enqueue
 
   uint32_t nqkv = 0;
   std::vector<uint8_t> have;  // which tensors are resident
@@ -342,6 +343,8 @@ struct Enq {
   uint32_t next_event = 0;
   uint64_t launches = 0;
   hipError_t first_error = hipSuccess;
+  uint32_t first_error_class = 0;
+  uint64_t first_error_launch = 0;
 
   template <typename F>
   void run(uint32_t cls, F&& f) {
@@ -353,7 +356,12 @@ struct Enq {
       hipEventRecord(b, ctx->stream);
     }
     hipError_t err = f();
-    if (err != hipSuccess && first_error == hipSuccess) first_error = err;
+    if (err != hipSuccess && first_error == hipSuccess) {
+      first_error = err;
+      first_error_class = cls;
+      first_error_launch = launches;
+    }
+    ++launches;
     if (b) {
       hipEventRecord(e, ctx->stream);
       ctx->prof_launches.push_back({cls, b, e});
@@ -447,6 +455,9 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   ++n;  // argmax is two launches
   *launches = n;
   ctx->step_launches = n;
+  if (q.first_error != hipSuccess)
+    ctx->launch_detail = std::string(" (kernel class ") + std::to_string(q.first_error_class) + ", launch " +
+                         std::to_string(q.first_error_launch) + ")";
   return q.first_error;
 }
 
@@ -913,7 +924,10 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     ++n;  // argmax is two launches
   }
   e = q.first_error;
-  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e));
+  if (e != hipSuccess)
+    return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + " (kernel class " +
+                                     std::to_string(q.first_error_class) + ", launch " +
+                                     std::to_string(q.first_error_launch) + ")");
   hipEventRecord(ctx->ev_end, s);
   if (nout) e = hipMemcpyAsync(p.h_out, p.choices, nout * 4, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipMemcpyAsync(p.h_out + kMaxPrefillOutputs, err, 4, hipMemcpyDeviceToHost, s);
@@ -990,7 +1004,7 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   } else {
     e = enqueue_step(ctx, nrows, &launches);
   }
-  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e));
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + ctx->launch_detail);
   hipEventRecord(ctx->ev_end, s);
   e = hipMemcpyAsync(ctx->h_out, ctx->choices, nrows * 4, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipMemcpyAsync(ctx->h_out + cap, ctx->err, 4, hipMemcpyDeviceToHost, s);

@@ -95,6 +95,15 @@ class PagePool:
             st = self.sequences[r.sequence]
             st.length = max(st.length, r.position + 1)
 
+    def truncate(self, sid: int, length: int) -> None:
+        """Commits a sequence to exactly `length` tokens: positions from
+        `length` on are a rejected suffix (written, unpublished, rewritten by
+        the next step). Reserved pages stay with the sequence."""
+        st = self.sequences[sid]
+        if length < 0 or (length + PAGE_TOKENS - 1) // PAGE_TOKENS > len(st.pages):
+            raise ValueError("commit end outside the reserved pages")
+        st.length = length
+
     def release(self, sid: int) -> None:
         st = self.sequences.pop(sid)
         self.free.extend(int(p) for p in st.pages)

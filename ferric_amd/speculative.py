@@ -1,0 +1,157 @@
+"""Greedy speculative decoding over two runners (a draft and a target model).
+
+Host orchestration of one speculative round with the reference's index
+contract (docs/M1_SPECULATIVE_KV_INDEXING.md; crates/ferric-spec/src/
+speculative_kv_indexing.rs:498-600) and greedy settlement
+(crates/ferric-spec/src/speculation.rs:126-200). For a round of width K at
+the shared cursor c with round anchor a (the last emitted token, not yet in
+either KV cache):
+
+  * draft: K decode steps; input 0 is a at position c, input i is the
+    candidate d[i-1] at position c + i; step i's choice is candidate d[i];
+  * target: one batch with the K + 1 inputs [a, d[0] .. d[K-1]] of every
+    sequence at positions c .. c + K (the token assembly of
+    ferric_qwen3_speculative_token_assembly_v1, logits.rs:587); choice i is
+    the target's greedy token after input i;
+  * settle: A = longest prefix with d[i] == t[i]; emitted = d[0..A) + t[A];
+  * commit: target to c + A + 1, draft to c + min(A + 1, K); the rest of
+    each tentative interval is a rejected suffix. t[A] is the next anchor.
+    When A == K the draft never consumed d[K-1]: the next round first runs
+    a draft catch-up step with d[K-1] at position c + K.
+
+The integer work (assembly, settlement) runs through the C ABI
+(fh_speculative_token_assembly, fh_verify_greedy_round).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import check, load
+from .pool import PagePool
+from .runner import TpBatchRunner
+
+
+@dataclass
+class SpecSequence:
+    target_sid: int
+    draft_sid: int
+    cursor: int  # committed tokens of the target (= the draft once caught up)
+    anchor: int  # last emitted token, not yet processed by either model
+    catch_up: int = -1  # draft candidate still to be consumed at cursor - 1, or -1
+    emitted: list = None
+
+
+@dataclass
+class RoundStats:
+    accepted: list
+    emitted: list
+    draft_steps: int
+    catch_up_rows: int
+    target_rows: int
+
+
+def _u32(a):
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+    return a, a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+
+
+def token_assembly(anchors, draft_iteration_major, k):
+    """target_ids[s][0] = anchors[s], target_ids[s][1 + i] = draft[i][s]."""
+    lib = load()
+    s = len(anchors)
+    a, ap = _u32(anchors)
+    d, dp = _u32(np.asarray(draft_iteration_major, dtype=np.uint32).reshape(-1) if k else [0])
+    out = np.zeros(s * (k + 1), dtype=np.uint32)
+    check(lib.fh_speculative_token_assembly(ap, dp if k else None, s, k,
+                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))))
+    return out.reshape(s, k + 1)
+
+
+def verify_greedy(draft, target):
+    """(accepted, emitted) of speculation.rs:126 for one sequence."""
+    lib = load()
+    d, dp = _u32(draft)
+    t, tp = _u32(target)
+    acc = ctypes.c_uint32()
+    em = (ctypes.c_uint32 * (len(draft) + 1))()
+    n = ctypes.c_uint32()
+    check(lib.fh_verify_greedy_round(dp if len(draft) else None, len(draft), tp, len(target), ctypes.byref(acc), em,
+                                     ctypes.byref(n)))
+    return int(acc.value), [int(x) for x in em[: n.value]]
+
+
+class SpeculativeDecoder:
+    """Greedy speculation of a draft runner for a target runner, each with
+    its own KV pool. Sequences share prompts and cursors across the two."""
+
+    def __init__(self, target: TpBatchRunner, target_pool: PagePool, draft: TpBatchRunner, draft_pool: PagePool,
+                 k: int = 4):
+        if k < 1:
+            raise ValueError("a speculative round needs at least one draft token")
+        self.target, self.tpool = target, target_pool
+        self.draft, self.dpool = draft, draft_pool
+        self.k = k
+        self.seqs: list[SpecSequence] = []
+
+    def _run(self, runner, pool, rows, outputs):
+        batch = pool.prepare(rows)
+        out = runner.execute_batch(batch, outputs)
+        pool.commit(batch)
+        return out.choices
+
+    def prefill(self, prompts):
+        """Prefills every prompt into both models (one batch each); the
+        target's greedy token after each prompt is the first anchor."""
+        t_rows, d_rows, outs = [], [], []
+        for p in prompts:
+            ts, ds = self.tpool.admit(0), self.dpool.admit(0)
+            self.seqs.append(SpecSequence(ts, ds, len(p), -1, emitted=[]))
+            t_rows += [(ts, int(x)) for x in p]
+            d_rows += [(ds, int(x)) for x in p]
+            outs.append(len(t_rows) - 1)
+        first = self._run(self.target, self.tpool, t_rows, outs)
+        self._run(self.draft, self.dpool, d_rows, [])
+        for s, tok in zip(self.seqs, first):
+            s.anchor = int(tok)
+            s.emitted.append(int(tok))
+        return first
+
+    def round(self) -> RoundStats:
+        k, seqs = self.k, self.seqs
+        # Draft catch-up: consume last round's final candidate where all were accepted.
+        late = [s for s in seqs if s.catch_up >= 0]
+        if late:
+            self._run(self.draft, self.dpool, [(s.draft_sid, s.catch_up) for s in late], [])
+            for s in late:
+                s.catch_up = -1
+        # K draft steps (decode batches of one row per sequence).
+        draft = np.zeros((k, len(seqs)), dtype=np.uint32)  # iteration-major
+        inputs = [s.anchor for s in seqs]
+        for i in range(k):
+            draft[i] = self._run(self.draft, self.dpool, [(s.draft_sid, int(t)) for s, t in zip(seqs, inputs)],
+                                 list(range(len(seqs))))
+            inputs = draft[i]
+        # One target batch of K + 1 inputs per sequence, every row an output row.
+        ids = token_assembly([s.anchor for s in seqs], draft, k)
+        rows = [(s.target_sid, int(t)) for s, row in zip(seqs, ids) for t in row]
+        batch = self.tpool.prepare(rows)
+        choices = np.asarray(self.target.execute_batch(batch, list(range(len(rows)))).choices,
+                             dtype=np.uint32).reshape(len(seqs), k + 1)
+        accepted, emitted = [], []
+        for j, s in enumerate(seqs):
+            a, em = verify_greedy(draft[:, j], choices[j])
+            c = s.cursor
+            self.tpool.truncate(s.target_sid, c + a + 1)
+            self.dpool.truncate(s.draft_sid, c + min(a + 1, k))
+            if a == k:
+                s.catch_up = int(draft[k - 1, j])
+            s.cursor = c + a + 1
+            s.anchor = em[-1]
+            s.emitted += em
+            accepted.append(a)
+            emitted.append(em)
+        return RoundStats(accepted, emitted, k, len(late), len(rows))
