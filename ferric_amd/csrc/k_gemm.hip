@@ -47,7 +47,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
                                                          uint32_t kb_count, uint32_t kb_split, uint32_t x_mtiles,
                                                          const uint16_t* residual, void* out, uint32_t ldo) {
   __shared__ float red[WAVES][NT * MT * 256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t tile0 = blockIdx.x * NT;
   const uint32_t split = blockIdx.y;
   const uint32_t s_lo = split * kb_split;
@@ -72,6 +72,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t steps = kb_hi - kb_lo;
+  const uint32_t chunks = steps / UNROLL;
+  // Each wave walks the whole-chunk part of its k-range starting at a
+  // rotated k-block (and wrapping). With every wave starting at the same
+  // aligned offset of its 1 KiB-tile streams, the concurrent loads of the
+  // grid fall on the same HBM channels and a 200 MB stream runs at ~5.2 TB/s
+  // instead of ~6.3; staggered starts spread them. The rotation depends on
+  // the launch coordinates only, so the summation order of an output does
+  // not depend on the batch's row count.
+  const uint32_t whole = chunks * UNROLL;
+  const uint32_t rot = whole ? ((blockIdx.x * WAVES + wave) * 7u + blockIdx.y * 5u) % whole : 0u;
   // Software pipeline over chunks of UNROLL k-blocks with two register sets:
   // the next chunk's loads are issued before the current chunk's MFMAs, and
   // scheduling barriers keep the compiler from sinking them back next to
@@ -80,10 +90,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
   auto load = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT], uint32_t s0) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
+      uint32_t sk = s0 + u + rot;
+      if (sk >= whole) sk -= whole;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)(s0 + u) * 64);
+      for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)sk * 64);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)(s0 + u) * xkb + mt * 64];
+      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)sk * xkb + mt * 64];
     }
   };
   auto compute = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT]) {
@@ -95,7 +107,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
         for (int mt = 0; mt < MT; ++mt)
           acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(wv[u][nt]), as_b8(xv[u][mt]), acc[nt][mt], 0, 0, 0);
   };
-  const uint32_t chunks = steps / UNROLL;
   if (chunks > 0) load(wa, xa, 0);
   for (uint32_t c = 0; c < chunks; c += 2) {
     if (c + 1 < chunks) load(wb, xb, (c + 1) * UNROLL);
@@ -198,19 +209,18 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
                        x_mtiles, residual, out, ldo);
 }
 
-// Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections):
-// weights of up to 16K rows use NT = 4 (activation traffic half the weight
-// traffic) with 8 waves at k <= 4096 and 4 waves at larger k; wider weights
-// (gate/up, LM head) have enough n-tiles to fill the chip, and NT = 2 keeps
-// twice as many workgroups in flight.
+// Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
+// cold weights): weights of up to 16K rows use NT = 4 (activation traffic
+// half the weight traffic) with 8 waves; the fused gate/up weight (24K rows)
+// keeps NT = 2 with 4 waves, twice as many workgroups in flight; the LM head
+// (152K rows) has n-tiles enough for NT = 4 with 4 waves.
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
   if (n % 64 == 0 && n < 16384) {
-    if (k <= 4096)
-      launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
-    else
-      launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+  } else if (EPI != FH_EPI_SWIGLU && n % 64 == 0) {
+    launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
   } else if (n % 32 == 0) {
     launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
   } else if constexpr (EPI != FH_EPI_SWIGLU) {

@@ -229,9 +229,16 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
   const uint32_t chunks = width / 8;
   constexpr int kMaxPerThread = 4;  // width <= 8192
   const uint64_t slab = (uint64_t)kMaxRows * width;
-  uint4 v[kMaxPerThread];
+  uint4 v[kMaxPerThread], wv[kMaxPerThread];
   float sum = 0.f;
   bool bad = false;
+  // The norm weight is loaded with the row, not after the reduction: one
+  // memory round trip less on this latency-bound kernel.
+#pragma unroll
+  for (int j = 0; j < kMaxPerThread; ++j) {
+    const uint32_t c = threadIdx.x + j * kNormThreads;
+    if (c < chunks) wv[j] = *reinterpret_cast<const uint4*>(w + c * 8);
+  }
 #pragma unroll
   for (int j = 0; j < kMaxPerThread; ++j) {
     const uint32_t c = threadIdx.x + j * kNormThreads;
@@ -292,9 +299,8 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
   for (int j = 0; j < kMaxPerThread; ++j) {
     const uint32_t c = threadIdx.x + j * kNormThreads;
     if (c < chunks) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + c * 8);
       const uint32_t xs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+      const uint32_t ws[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
       uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
