@@ -10,6 +10,10 @@
 // narrows once. This kernel pair keeps that contract with kAttnSplitPages-page
 // partitions.
 //
+// K and V are read once per step, so their loads are non-temporal: letting
+// them allocate in the caches cost about 13% of the kernel's time (measured
+// with 32 rows of mean context 4K, 550 MB of K/V per layer).
+//
 // Partition kernel, grid (partition, KV head, row), 4 waves; each wave takes
 // 4 of the partition's 16 pages and the G query heads of the KV head, so
 // every K/V byte is read once per token row. A wave makes two memory round
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
         const uint32_t* vp =
             reinterpret_cast<const uint32_t*>(vc + (((uint64_t)phys_of(u) * 16) * kvh + h) * 128) + lane;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) vd[u][e] = vp[e * vstride];
+        for (int e = 0; e < 16; ++e) vd[u][e] = __builtin_nontemporal_load(vp + e * vstride);
       }
     }
   };
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
         const uint16_t* kp = kc + (((uint64_t)phys_of(u) * 16 + g16) * kvh + h) * 128 + 8 * r16;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          kr[u][i] = *reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128);
+          kr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128));
       }
     }
 #pragma unroll
