@@ -14,8 +14,8 @@
 // them allocate in the caches cost about 13% of the kernel's time (measured
 // with 32 rows of mean context 4K, 550 MB of K/V per layer).
 //
-// Partition kernel, grid (partition, KV head, row), 4 waves; each wave takes
-// 4 of the partition's 16 pages and the G query heads of the KV head, so
+// Partition kernel, grid (partition, KV head, row), 8 waves; each wave takes
+// 4 of the partition's 32 pages and the G query heads of the KV head, so
 // every K/V byte is read once per token row. A wave makes two memory round
 // trips, each with all of its pages' loads in flight at once:
 //   1. K: whole 256-byte token rows per load, re-laid through a padded LDS
@@ -25,7 +25,7 @@
 //   2. Exact softmax over the wave's 64 tokens (max, p = exp(s - max), sum),
 //      then PV on VALU: lane l owns output dims 2l, 2l+1, and a token's V row
 //      is one coalesced 256-byte wave load.
-// The four wave states (m, l, n[128]) are merged in wave order. A row whose
+// The eight wave states (m, l, n[128]) are merged in wave order. A row whose
 // context fits one partition is finished here (divide, narrow, store);
 // longer rows leave partition states for the merge kernel.
 // Merge kernel: one wave per (row, query head). Partition weights
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
   if (!(L > 0.f) || ((o0 & 0x7f80u) == 0x7f80u) || ((o1 & 0x7f80u) == 0x7f80u)) raise_error(err, ERR_NONFINITE);
 }
 
-template <int G, int WAVES = 4>
+template <int G, int WAVES = 8>
 void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                       const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
                       uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,

@@ -11,11 +11,8 @@ namespace fh {
 void set_thread_error(const char* msg);
 
 // Attention partition: each partition workgroup covers this many pages of
-// 16 tokens (every wave of the workgroup walks all of them for its KV head).
-#ifndef FH_ATTN_SPLIT_PAGES
-#define FH_ATTN_SPLIT_PAGES 16
-#endif
-constexpr uint32_t kAttnSplitPages = FH_ATTN_SPLIT_PAGES;
+// 16 tokens (its 8 waves take 4 pages each).
+constexpr uint32_t kAttnSplitPages = 32;
 constexpr uint32_t kAttnSplitTokens = kAttnSplitPages * 16;
 // Floats per attention partial record: running max, denominator, numerator[128].
 constexpr uint32_t kAttnPartialFloats = 2 + 128;
