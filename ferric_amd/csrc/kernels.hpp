@@ -90,6 +90,17 @@ hipError_t launch_attention_merge(const float* partials, const uint32_t* positio
                                   uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
                                   uint32_t context, uint32_t* err, hipStream_t s);
 
+// Prefill attention over blocks of consecutive rows of one sequence (see
+// k_attention_block.hip). blocks[i] = first row | (rows << 16); each block
+// has at most attention_block_rows(qh, kvh) rows at consecutive positions,
+// and its last row's page table serves all of them. No scratch, no merge.
+uint32_t attention_block_rows(uint32_t qh, uint32_t kvh);
+hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                   const uint32_t* positions, const uint32_t* table, const uint32_t* blocks,
+                                   uint32_t nblocks, uint16_t* out, uint32_t out_tiled, uint32_t out_rows,
+                                   uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                                   uint32_t* err, hipStream_t s);
+
 // logits
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
                          uint32_t* err, hipStream_t s);

@@ -27,7 +27,6 @@ constexpr uint32_t kPageTokens = 16;
 constexpr uint32_t kMaxRows = 32;
 // Prefill chunks: attention runs over this many rows per launch pair (bounds
 // the partition-state scratch), and at most this many output rows get logits.
-constexpr uint32_t kPrefillAttnRows = 256;
 constexpr uint32_t kMaxPrefillOutputs = 256;
 
 thread_local std::string g_create_error;
@@ -99,13 +98,12 @@ struct fh_ctx {
     uint16_t* qrot = nullptr;      // [rows][qh*128]
     uint16_t* attn = nullptr;      // tiled
     uint16_t* act = nullptr;       // tiled
-    float* attn_part = nullptr;    // partition states of kPrefillAttnRows rows
     uint16_t* out_hidden = nullptr;  // gathered output rows [kMaxPrefillOutputs][hidden]
     uint16_t* out_xn = nullptr;    // tiled
     float* logits = nullptr;       // [kMaxPrefillOutputs][vocab]
     void* argmax_scratch = nullptr;
     uint32_t* choices = nullptr;
-    uint32_t* d_meta = nullptr;    // tokens[P] | positions[P] | output rows[kMaxPrefillOutputs] | table[P][stride]
+    uint32_t* d_meta = nullptr;    // tokens[P] | positions[P] | output rows[kMaxPrefillOutputs] | blocks[P] | table[P][stride]
     uint32_t* h_meta = nullptr;
     uint32_t* h_out = nullptr;     // choices[kMaxPrefillOutputs] | error word
   } pre;
@@ -592,14 +590,12 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
     TRY(dalloc(ctx, &p.qrot, (uint64_t)P * Q));
     TRY(dalloc(ctx, &p.attn, tiled_rows * Q));
     TRY(dalloc(ctx, &p.act, tiled_rows * I));
-    TRY(dalloc(ctx, &p.attn_part, (uint64_t)kPrefillAttnRows * md.query_heads * fh::attn_max_splits(op.context_tokens) *
-                                      fh::kAttnPartialFloats));
     TRY(dalloc(ctx, &p.out_hidden, (uint64_t)kMaxPrefillOutputs * H));
     TRY(dalloc(ctx, &p.out_xn, out_tiled_rows * H));
     TRY(dalloc(ctx, &p.logits, (uint64_t)kMaxPrefillOutputs * V));
     TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&p.argmax_scratch), fh_argmax_scratch_bytes(kMaxPrefillOutputs)));
     TRY(dalloc(ctx, &p.choices, kMaxPrefillOutputs));
-    const uint64_t pmeta = 2ull * P + kMaxPrefillOutputs + (uint64_t)P * op.page_table_stride;
+    const uint64_t pmeta = 3ull * P + kMaxPrefillOutputs + (uint64_t)P * op.page_table_stride;
     TRY(dalloc(ctx, &p.d_meta, pmeta));
     TRY(halloc(ctx, &p.h_meta, pmeta));
     TRY(halloc(ctx, &p.h_out, kMaxPrefillOutputs + 1));
@@ -818,9 +814,10 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
 
 // A prefill chunk (row_capacity < nrows <= prefill_rows), launched eagerly:
 // the decode path's op order (batched.rs:1746-2454) with the compute-bound
-// projections, bf16 QKV rows into the QK-norm kernel, attention in row
-// blocks of kPrefillAttnRows, and the final norm + FP32 head + argmax over
-// the requested output rows only.
+// projections, bf16 QKV rows into the QK-norm kernel, attention over blocks
+// of consecutive rows of one sequence (each K/V page read once per block),
+// and the final norm + FP32 head + argmax over the requested output rows
+// only.
 fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
                       const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
   const fh_model_desc& md = ctx->md;
@@ -832,7 +829,8 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   uint32_t* tok = p.h_meta;
   uint32_t* pos = p.h_meta + P;
   uint32_t* outs = p.h_meta + 2 * P;
-  uint32_t* tab = p.h_meta + 2 * P + kMaxPrefillOutputs;
+  uint32_t* blocks = p.h_meta + 2 * P + kMaxPrefillOutputs;
+  uint32_t* tab = p.h_meta + 3 * P + kMaxPrefillOutputs;
   for (uint32_t i = 0; i < nrows; ++i) {
     tok[i] = rows[i].token;
     pos[i] = rows[i].position;
@@ -841,9 +839,20 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
   }
   for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
-  std::vector<uint32_t> block_max_pos((nrows + kPrefillAttnRows - 1) / kPrefillAttnRows, 0);
-  for (uint32_t i = 0; i < nrows; ++i)
-    block_max_pos[i / kPrefillAttnRows] = std::max(block_max_pos[i / kPrefillAttnRows], rows[i].position);
+  // Attention blocks: runs of rows of one sequence at consecutive positions
+  // whose page lists extend one another (so the block's last row's table
+  // serves every row of it), at most attention_block_rows() rows each.
+  const uint32_t bq = fh::attention_block_rows(QH, KVH);
+  uint32_t nblocks = 0;
+  for (uint32_t i = 0; i < nrows;) {
+    uint32_t j = i + 1;
+    while (j < nrows && j - i < bq && rows[j].sequence == rows[i].sequence &&
+           rows[j].position == rows[j - 1].position + 1 && rows[j].page_count >= rows[j - 1].page_count &&
+           std::memcmp(rows[j].pages, rows[j - 1].pages, (size_t)rows[j - 1].page_count * 4) == 0)
+      ++j;
+    blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
+    i = j;
+  }
   auto poison = [&](fh_status s2, const std::string& msg) {
     ctx->poisoned = true;
     return fail(ctx, s2, msg);
@@ -852,8 +861,9 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   const uint32_t* d_tok = p.d_meta;
   const uint32_t* d_pos = p.d_meta + P;
   const uint32_t* d_out = p.d_meta + 2 * P;
-  const uint32_t* d_tab = p.d_meta + 2 * P + kMaxPrefillOutputs;
-  const uint64_t meta_bytes = (2ull * P + kMaxPrefillOutputs + (uint64_t)nrows * stride) * 4;
+  const uint32_t* d_blocks = p.d_meta + 2 * P + kMaxPrefillOutputs;
+  const uint32_t* d_tab = p.d_meta + 3 * P + kMaxPrefillOutputs;
+  const uint64_t meta_bytes = (3ull * P + kMaxPrefillOutputs + (uint64_t)nrows * stride) * 4;
   hipError_t e = hipMemcpyAsync(p.d_meta, p.h_meta, meta_bytes, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("metadata upload: ") + hipGetErrorString(e));
   hipEventRecord(ctx->ev_begin, s);
@@ -883,19 +893,10 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
       return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
                                        p.qrot, kc, vc, R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
     });
-    for (uint32_t r0 = 0; r0 < R; r0 += kPrefillAttnRows) {
-      const uint32_t rn = std::min(kPrefillAttnRows, R - r0);
-      L(FH_KC_ATTENTION, [&] {
-        return fh::launch_attention_partial(p.qrot + (uint64_t)r0 * Q, kc, vc, d_pos + r0,
-                                            d_tab + (uint64_t)r0 * stride, p.attn_part, p.attn, 1, r0, R, rn, QH, KVH,
-                                            stride, pages, C, err, s);
-      });
-      // Rows whose context fits one partition finish in the partition kernel.
-      if (block_max_pos[r0 / kPrefillAttnRows] >= fh::kAttnSplitTokens)
-        L(FH_KC_ATTENTION_MERGE, [&] {
-          return fh::launch_attention_merge(p.attn_part, d_pos + r0, p.attn, 1, r0, R, rn, QH, C, err, s);
-        });
-    }
+    L(FH_KC_ATTENTION, [&] {
+      return fh::launch_attention_blocks(p.qrot, kc, vc, d_pos, d_tab, d_blocks, nblocks, p.attn, 1, R, QH, KVH,
+                                         stride, pages, C, err, s);
+    });
     L(FH_KC_O_GEMM, [&] {
       return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);
     });
@@ -1051,8 +1052,7 @@ fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled) {
   if (!ctx) return FH_ERR_INVALID_ARGUMENT;
   ctx->profiling = enabled != 0;
   if (ctx->profiling && ctx->prof_events.empty()) {
-    const uint64_t attn_blocks = ctx->opt.prefill_rows ? (ctx->opt.prefill_rows + kPrefillAttnRows - 1) / kPrefillAttnRows : 1;
-    const uint64_t need = 2 * (12 + (10ull + 2 * attn_blocks) * ctx->md.layers);
+    const uint64_t need = 2 * (12 + 12ull * ctx->md.layers);
     for (uint64_t i = 0; i < need; ++i) {
       hipEvent_t ev;
       FH_HIP(ctx, hipEventCreate(&ev));

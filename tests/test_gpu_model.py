@@ -359,6 +359,32 @@ def test_prefill_chunk_8b_layer_shapes():
     _prefill_case(cfg, limits, [40], [100, 3000], 64, 37, "prefill 8b")
 
 
+def test_prefill_continuation_and_interleaved_rows():
+    # 0.6B shape, 2 layers. Prefill attention groups runs of rows of one
+    # sequence at consecutive positions into blocks: a 70-row continuation of
+    # a 300-token sequence (blocks starting mid-page, a long prefix in every
+    # block), then three sequences' rows interleaved one by one (every block
+    # a single row), one of them a new prompt from position 0.
+    cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
+    limits = PagedLimits(context_tokens=2048, physical_page_count=400, page_table_stride=128)
+    pair = Pair(cfg, limits, seed=41, capture=False, rows=8, prefill_rows=256)
+    try:
+        rng = np.random.default_rng(41)
+        a, b = pair.admit_with_prefix([300, 37])
+        c = pair.pool.admit(0)
+        rows = [(a, int(t)) for t in rng.integers(0, cfg["vocabulary"], 70)]
+        for _ in range(12):
+            for sid in (b, c, a):
+                rows.append((sid, int(rng.integers(0, cfg["vocabulary"]))))
+        outs = [0, 33, 69, 70, 71, 72, len(rows) - 3, len(rows) - 2, len(rows) - 1]
+        batch, out, ref = pair.step(rows, outs)
+        _mark_written(pair, batch)
+        pair.check(batch, out, ref, "continuation + interleaved prefill")
+        pair.check_kv()
+    finally:
+        pair.close()
+
+
 @pytest.mark.parametrize("same_draft", [True, False])
 def test_speculative_rounds_emit_the_target_greedy_stream(same_draft):
     # Target and draft: 0.6B shape, 2 layers. With identical weights the draft
