@@ -308,6 +308,22 @@ def speculative_bench(args, name):
     print(json.dumps(result), flush=True)
 
 
+TRAFFIC_PROFILE = "profiles/attention_decode_qwen3_8b_b32_hbm_counters.md"
+
+
+def measured_traffic(workload):
+    """HBM bytes per attention launch of the default workload, as measured by the
+    FETCH_SIZE / WRITE_SIZE passes summarised in TRAFFIC_PROFILE (None if absent)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE)
+    if workload != "qwen3-8b-b32" or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("| `attn_partition_kernel"):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            return int(float(cells[3]) * 1e6)
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -386,6 +402,12 @@ def main():
                 per_layer = 2 * cfg["layers"] + 1
             class_bytes[k] = class_bytes.get(k, 0) + b * per_layer
     runner.set_profiling(False)
+    # The dominant kernel's launch duration without an event pair around it:
+    # the last step's attention re-launched back to back (same inputs).
+    attn_timing = None
+    if args.profile_steps > 0:
+        attn_timing = (runner.time_attention(20),
+                       kernel_bytes(cfg, batch, positions, limits.page_table_stride)["attention"])
 
     ms_per_step = elapsed * 1e3 / args.steps
     value = batch * args.steps / elapsed
@@ -416,11 +438,18 @@ def main():
         dominant = max(class_ms, key=lambda k: class_ms[k])
         avg_ms = class_ms[dominant] / max(class_launches[dominant], 1)
         bytes_per_launch = class_bytes.get(dominant, 0) / max(class_launches[dominant], 1)
+        timing = "HIP events around each launch of the profiled eager steps"
+        if dominant == "attention" and attn_timing:
+            avg_ms, bytes_per_launch = attn_timing
+            timing = "last layer's attention launch of the last step, re-run 20 times back to back between HIP events"
         achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+        traffic = measured_traffic(name) if dominant == "attention" else None
         result["roofline"] = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
                               "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                              "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 2),
-                              "algorithmic_bytes_per_launch": int(bytes_per_launch)}
+                              "traffic": traffic, "avg_launch_us": round(avg_ms * 1e3, 2),
+                              "algorithmic_bytes_per_launch": int(bytes_per_launch), "timing": timing}
+        if traffic:
+            result["roofline"]["traffic_source"] = TRAFFIC_PROFILE
         result["kernels"] = {
             k: {"ms_per_step": round(class_ms[k] / args.profile_steps, 4),
                 "gbs": round(class_bytes.get(k, 0) / (class_ms[k] * 1e-3) / 1e9, 1) if class_ms[k] > 0 else None}

@@ -1,7 +1,7 @@
 """ctypes binding of libferric_hip.so (the C ABI in include/ferric_hip.h).
 
 There is no fallback: if the library is missing or cannot be loaded, import
-fails with the reason. Build it with `python -m ferric_amd.build` (or
+fails with the reason. Build it with `python ferric_amd/build.py` (or
 __graft_entry__.build()).
 """
 
@@ -116,6 +116,7 @@ SIGNATURES = [
     ("fh_last_step_ms", ctypes.c_float, [_vp]),
     ("fh_set_profiling", _st, [_vp, _u32]),
     ("fh_kernel_class_ms", _st, [_vp, _u32, _f32p, _u32p]),
+    ("fh_time_attention", _st, [_vp, _u32, _f32p]),
     ("fh_op_tile_weight", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_tile_gate_up", _st, [_vp, _vp, _vp, _u32, _u32, _vp]),
     ("fh_op_untile_weight", _st, [_vp, _vp, _u32, _u32, _vp]),
@@ -147,7 +148,7 @@ def load() -> ctypes.CDLL:
     if _lib is not None:
         return _lib
     if not LIBRARY.exists():
-        raise ImportError(f"{LIBRARY} is not built; run `python -m ferric_amd.build` (hipcc, gfx950)")
+        raise ImportError(f"{LIBRARY} is not built; run `python ferric_amd/build.py` (hipcc, gfx950)")
     # PyTorch ships its own libamdhip64 under the same soname. Loading torch
     # first makes this library bind to that copy; the other order maps two
     # HIP runtimes into the process, and the second one to touch the device

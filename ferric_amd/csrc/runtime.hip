@@ -1062,6 +1062,42 @@ fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled) {
   return FH_OK;
 }
 
+fh_status fh_time_attention(fh_ctx* ctx, uint32_t reps, float* avg_ms) {
+  if (!ctx || !avg_ms || reps == 0 || reps > 1000) return FH_ERR_INVALID_ARGUMENT;
+  if (ctx->poisoned) return fail(ctx, FH_ERR_POISONED, "runtime poisoned by an earlier failure");
+  if (ctx->last_was_prefill || ctx->last_rows == 0) return fail(ctx, FH_ERR_STATE, "no decode batch to time");
+  const fh_model_desc& md = ctx->md;
+  const fh_ctx_options& op = ctx->opt;
+  const uint32_t R = ctx->last_rows, cap = op.row_capacity, l = md.layers - 1;
+  const uint32_t* d_pos = ctx->d_meta + cap;
+  const uint32_t* d_tab = ctx->d_meta + 2 * cap;
+  hipStream_t s = ctx->stream;
+  auto launch = [&] {
+    return fh::launch_attention_partial(ctx->qrot, kv_cache(ctx, l, 0), kv_cache(ctx, l, 1), d_pos, d_tab,
+                                        ctx->attn_part, ctx->attn, 1, 0, R, R, md.query_heads, md.kv_heads,
+                                        op.page_table_stride, op.physical_pages, op.context_tokens, ctx->err, s);
+  };
+  hipEvent_t a = nullptr, b = nullptr;
+  (void)hipGetLastError();
+  hipError_t e = hipEventCreate(&a);
+  if (e == hipSuccess) e = hipEventCreate(&b);
+  if (e == hipSuccess) e = launch();  // warm: same inputs, so the same outputs as the step wrote
+  if (e == hipSuccess) e = hipEventRecord(a, s);
+  for (uint32_t i = 0; i < reps && e == hipSuccess; ++i) e = launch();
+  if (e == hipSuccess) e = hipEventRecord(b, s);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+  if (a) hipEventDestroy(a);
+  if (b) hipEventDestroy(b);
+  if (e != hipSuccess) {
+    ctx->poisoned = true;
+    return fail(ctx, FH_ERR_DEVICE, std::string("attention timing: ") + hipGetErrorString(e));
+  }
+  *avg_ms = ms / (float)reps;
+  return FH_OK;
+}
+
 fh_status fh_kernel_class_ms(const fh_ctx* ctx, uint32_t cls, float* ms, uint32_t* launches) {
   if (!ctx || cls >= FH_KC_COUNT || !ms || !launches) return FH_ERR_INVALID_ARGUMENT;
   *ms = ctx->class_ms[cls];

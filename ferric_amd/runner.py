@@ -223,6 +223,12 @@ class TpBatchRunner:
     def set_profiling(self, enabled: bool) -> None:
         check(self._lib.fh_set_profiling(self._ctx, 1 if enabled else 0), self._ctx)
 
+    def time_attention(self, reps: int = 20) -> float:
+        """Mean ms of the last decode batch's attention launch, re-run back to back."""
+        ms = ctypes.c_float()
+        check(self._lib.fh_time_attention(self._ctx, reps, ctypes.byref(ms)), self._ctx)
+        return float(ms.value)
+
     def kernel_class_ms(self) -> dict:
         out = {}
         for i, name in enumerate(_lib.KERNEL_CLASSES):

@@ -170,6 +170,12 @@ float fh_last_step_ms(const fh_ctx* ctx);
  * kernel_class indexes fh_kernel_class; returns total ms across launches of that class. */
 fh_status fh_set_profiling(fh_ctx* ctx, uint32_t enabled);
 fh_status fh_kernel_class_ms(const fh_ctx* ctx, uint32_t kernel_class, float* ms, uint32_t* launches);
+/* Measurement aid with no counterpart in the reference: re-launches the last decode
+ * batch's attention partition kernel for the last layer (same inputs, so it rewrites the
+ * same outputs) reps times back to back on the context stream between two events and
+ * writes the mean launch duration in ms (1 <= reps <= 1000). FH_ERR_STATE if the last
+ * batch was not a decode batch. */
+fh_status fh_time_attention(fh_ctx* ctx, uint32_t reps, float* avg_ms);
 
 typedef enum fh_kernel_class {
   FH_KC_EMBEDDING = 0,

@@ -111,6 +111,8 @@ def test_ops_reject_bad_shapes_before_any_launch():
     assert lib.fh_op_tile_activation(p, p, 33, 48, None) == 1  # k % 32
     assert lib.fh_activation_rows(1) == 32 and lib.fh_activation_rows(32) == 32
     assert lib.fh_activation_rows(33) == 256 and lib.fh_activation_rows(257) == 512
+    ms = ctypes.c_float()
+    assert lib.fh_time_attention(None, 1, ctypes.byref(ms)) == 1  # no context
     assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1
     assert lib.fh_op_residual_rmsnorm(p, None, 2, p, p, 1, 4, 4096, 1e-6, None, None) == 1  # partials missing
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
