@@ -22,7 +22,8 @@
 //      tile into the MFMA A operand (lane l: token l % 16, dims 32 i + 8 (l/16)
 //      for MFMA i); S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the G queries
 //      as the B operand; scaled, masked scores go to LDS.
-//   2. Exact softmax over the wave's 64 tokens (max, p = exp(s - max), sum),
+//   2. V loads issued as soon as the scores are out, in flight during the
+//      exact softmax over the wave's 64 tokens (max, p = exp(s - max), sum);
 //      then PV on VALU: lane l owns output dims 2l, 2l+1, and a token's V row
 //      is one coalesced 256-byte wave load.
 // The eight wave states (m, l, n[128]) are merged in wave order. A row whose
@@ -81,6 +82,14 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
   // The wave index is uniform; saying so keeps every page address scalar.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t p0 = split * kAttnSplitPages;
+  // This wave's pages: [w0, w0 + np) of the row. The page-table entries are
+  // requested together with the position (they do not depend on it), so the
+  // K loads wait for one memory round trip, not two.
+  const uint32_t w0 = p0 + wave * kWavePages;
+  const uint32_t* trow = table + (uint64_t)r * stride;
+  static_assert(kWavePages <= 64, "one page-table entry per lane");
+  const uint32_t raw_phys = lane < (int)kWavePages && w0 + lane < stride ? trow[w0 + lane] : 0u;
   const uint32_t pos = positions[r];
   if (pos >= context || pos / 16 >= stride) {
     if (split == 0 && h == 0 && threadIdx.x == 0) raise_error(err, ERR_POSITION);
@@ -88,11 +97,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   }
   const uint32_t ctx = pos + 1;
   const uint32_t row_pages = (ctx + 15) / 16;
-  const uint32_t p0 = split * kAttnSplitPages;
   if (p0 >= row_pages) return;  // uniform per workgroup
   const uint32_t nsplit = (row_pages + kAttnSplitPages - 1) / kAttnSplitPages;
-  // This wave's pages: [w0, w0 + np) of the row.
-  const uint32_t w0 = p0 + wave * kWavePages;
   const uint32_t np = w0 < row_pages ? min(row_pages - w0, kWavePages) : 0u;
 
   // Scores of the wave's tokens, replaced in place by probabilities: [token][g].
@@ -104,7 +110,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   const int g16 = lane >> 4, r16 = lane & 15;
   const float scale = __builtin_bit_cast(float, kScaleBits);
   const float kNegInf = -__builtin_inff();
-  const uint32_t* trow = table + (uint64_t)r * stride;
   bool bad = false;
 
   // B operand: query head h*G + r16 (zero for r16 >= G); MFMA i, lane group
@@ -121,8 +126,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
 
   // Physical pages of this wave, one per lane, read back with readlane so no
   // scalar table load sits between page loads.
-  static_assert(kWavePages <= 64, "one page-table entry per lane");
-  uint32_t my_phys = lane < (int)np ? trow[w0 + lane] : 0u;
+  uint32_t my_phys = lane < (int)np ? raw_phys : 0u;
   if (my_phys >= pages) {
     bad = true;
     my_phys = 0;
@@ -196,6 +200,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
       }
     }
   }
+  // V loads go out now, so they are in flight during the softmax.
+  load_v();
   pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
   pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
   float m[G], l[G], acc[G][2];
@@ -232,7 +238,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   // Pass 2: n += p * v on VALU; lane l owns output dims 2l, 2l+1, and a
   // token's V row is one coalesced 256-byte wave load.
   {
-    load_v();
     auto pv_page = [&](auto full_tag, uint32_t u) {
       constexpr bool FULL = decltype(full_tag)::value;
       const uint32_t valid = FULL ? 16u : min(16u, ctx - (w0 + u) * 16);
