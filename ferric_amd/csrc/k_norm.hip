@@ -422,6 +422,89 @@ __global__ __launch_bounds__(256, 2) void qknorm_rope_kv_rows_kernel(
   if (bad) raise_error(err, ERR_NONFINITE);
 }
 
+// RMSNorm of many rows into activation tile order (the prefill path, no
+// split-K partials): one 512-thread workgroup per 16-row tile. Thread t
+// handles the tile-order chunks q = 512 j + t of its row tile (k-block
+// q / 64, in-tile lane q % 64, i.e. row q % 16, columns 32 (q / 64) +
+// 8 ((q % 64) / 16)), so every wave writes whole 1 KiB tiles and reads 64
+// contiguous bytes of each of 16 rows (a tile written piecewise by
+// different waves would cost partial-line writes). All of a thread's
+// chunks belong to row t % 16: the row's sum of squares is the thread
+// partials (chunks in ascending j) added over t = r, r + 16, ... in order.
+// width % 32 == 0, width <= 4096.
+constexpr uint32_t kTileRows = 16;
+constexpr int kTileThreads = 512;
+constexpr int kRowsMaxChunks = 4096 / 8 * kTileRows / kTileThreads;  // 16
+
+__global__ __launch_bounds__(kTileThreads) void rmsnorm_tile_rows_kernel(const uint16_t* __restrict__ x,
+                                                                         const uint16_t* __restrict__ w,
+                                                                         uint16_t* __restrict__ y, uint32_t rows,
+                                                                         uint32_t y_mtiles, uint32_t width, float eps,
+                                                                         uint32_t* err) {
+  __shared__ float part[kTileThreads];
+  __shared__ float inv_s[kTileRows];
+  __shared__ uint32_t bad_s;
+  const uint32_t t = threadIdx.x, mt = blockIdx.x, row0 = mt * kTileRows;
+  const uint32_t lane = t & 63u, r = lane & 15u, g = lane >> 4;
+  const uint32_t kbs = width / 32;  // k-blocks per row
+  const bool live = row0 + r < rows;
+  if (t == 0) bad_s = 0;
+  uint4 v[kRowsMaxChunks];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRowsMaxChunks; ++j) {
+    const uint32_t kb = j * (kTileThreads / 64) + (t >> 6);
+    if (kb < kbs && live) {
+      v[j] = *reinterpret_cast<const uint4*>(x + (uint64_t)(row0 + r) * width + kb * 32 + g * 8);
+      const uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a = lo_bf16(words[k]), b = hi_bf16(words[k]);
+        sum = sum + a * a;
+        sum = sum + b * b;
+      }
+    } else {
+      v[j] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  part[t] = sum;
+  __syncthreads();
+  if (t < kTileRows) {
+    float s2 = part[t];
+    for (uint32_t i = 1; i < kTileThreads / kTileRows; ++i) s2 = s2 + part[t + kTileRows * i];
+    const float inv = inverse_rms(s2, (float)width, eps);
+    inv_s[t] = inv;
+    if (row0 + t < rows && (!is_finite_f32(s2) || !is_finite_f32(inv))) bad_s = 1;
+  }
+  __syncthreads();
+  bool bad = false;
+  const float inv = inv_s[r];
+#pragma unroll
+  for (int j = 0; j < kRowsMaxChunks; ++j) {
+    const uint32_t kb = j * (kTileThreads / 64) + (t >> 6);
+    if (kb < kbs) {
+      uint32_t o[4] = {0u, 0u, 0u, 0u};
+      if (live) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(w + kb * 32 + g * 8);
+        const uint32_t xs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t a = norm_weight_bf16(lo_bf16(xs[k]), inv, lo_bf16(ws[k]));
+          const uint32_t b = norm_weight_bf16(hi_bf16(xs[k]), inv, hi_bf16(ws[k]));
+          bad |= ((a & 0x7f80u) == 0x7f80u) | ((b & 0x7f80u) == 0x7f80u);
+          o[k] = a | (b << 16);
+        }
+      }
+      // Rows past the batch in the last tile are written as zeros (the tiled
+      // buffer's padding rows, which the projections read and never use).
+      *reinterpret_cast<uint4*>(y + (((uint64_t)kb * y_mtiles + mt) * 64 + lane) * 8) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  if (bad || (t == 0 && bad_s)) raise_error(err, ERR_NONFINITE);
+}
+
 // Row-major <-> activation tile order, one 16-byte chunk per thread.
 __global__ __launch_bounds__(kNormThreads) void tile_activation_kernel(const uint16_t* __restrict__ x,
                                                                        uint16_t* __restrict__ xt, uint32_t m,
@@ -491,6 +574,11 @@ hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uin
 hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* w,
                                    uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float eps,
                                    uint32_t* err, hipStream_t s) {
+  if (!partials && y_tiled && rows > kMaxRows && width % 32 == 0 && width <= 4096) {
+    hipLaunchKernelGGL(rmsnorm_tile_rows_kernel, dim3((rows + kTileRows - 1) / kTileRows), dim3(kTileThreads), 0, s,
+                       hidden, w, y, rows, act_mtiles(rows), width, eps, err);
+    return hipGetLastError();
+  }
 #define FH_RESNORM(S_)                                                                                             \
   hipLaunchKernelGGL(residual_rmsnorm_kernel<S_>, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, \
                      y, y_tiled ? act_mtiles(rows) : 0u, width, eps, err)
