@@ -369,7 +369,7 @@ def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
         # a prefill-size batch: 40 rows, tiled output of fh_activation_rows(40) rows
         positions = r.integers(0, 2000, 40).astype(np.uint32)
     else:
-        # one partition (<= 256 tokens), several partitions, page-boundary and partial-page cases
+        # one partition (<= 512 tokens), several partitions, page-boundary and partial-page cases
         positions = np.array([0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 8319, 77, 8190, 6000], np.uint32)
     rows = len(positions)
     kc, vc = _paged_pool(r, pages, kvh)
@@ -400,6 +400,36 @@ def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
             if positions[i] == 0:
                 # one key: softmax weight 1, output = V row bits exactly
                 assert np.array_equal(got[i, h], ref)
+    assert worst <= 1e-2, worst
+
+
+def test_paged_attention_long_context():
+    # 40960-token context: up to 80 partitions per row, more than one 64-lane
+    # chunk of partition weights in the merge; a page table of 2560 entries.
+    r = rng(4242)
+    qh, kvh = 32, 8
+    pages, stride, context = 2600, 2560, 40960
+    positions = np.array([40959, 32767, 32768, 16384, 511, 512, 0, 40000], np.uint32)
+    rows = len(positions)
+    kc, vc = _paged_pool(r, pages, kvh)
+    q = rand_bf16(r, rows * qh * 128, 1.0)
+    table = np.stack([r.permutation(pages)[:stride] for _ in range(rows)]).astype(np.uint32)
+    scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
+    out = du.empty(rows * qh * 128, np.uint16)
+    err = du.empty(1, np.uint32)
+    dkc, dvc = du.to_dev(kc), du.to_dev(vc)
+    dq, dpos, dtab = du.to_dev(q), du.to_dev(positions), du.to_dev(table)
+    _lib.check(LIB.fh_op_paged_attention(du.ptr(dq), du.ptr(dkc), du.ptr(dvc), du.ptr(dpos), du.ptr(dtab),
+                                         du.ptr(out), 0, du.ptr(scratch), rows, qh, kvh, stride, pages, context,
+                                         du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    got = du.to_host(out, np.uint16).reshape(rows, qh, 128)
+    worst = 0.0
+    for i in range(rows):
+        for h in range(0, qh, 5):  # a spread of query heads over every KV head
+            ref = orc.attention_head(q[(i * qh + h) * 128:(i * qh + h + 1) * 128], kc, vc, table[i], pages,
+                                     int(positions[i]), kvh, h // (qh // kvh))
+            worst = max(worst, du.bf16_rel_err(got[i, h], ref))
     assert worst <= 1e-2, worst
 
 
