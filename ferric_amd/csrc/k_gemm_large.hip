@@ -197,11 +197,15 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
 
   // Issue order per iteration j: W(j + 3), then X(j + 2). At iteration kb,
   // X(kb) was issued two iterations back and W(kb + 2), X(kb + 1) after it:
-  // 2 + 4 = 6 loads may stay in flight.
+  // 2 + 4 = 6 loads may stay in flight. The prologue issues in the same
+  // order (W0 W1 X0 W2 X1), so the first iteration's wait covers X0 as well;
+  // with W2 after X0 the compiler had to add its own wait for X0 inside the
+  // loop, and with direct-to-LDS loads in flight that wait is vmcnt(0),
+  // which drained every load once per 3 k-blocks.
   fetch_w(0);
   fetch_w(1);
-  fetch_w(2);
   FH_XD_LOADX(0, 0);
+  fetch_w(2);
   FH_XD_LOADX(1, 1);
 #define FH_XD_STEP(KB, S)                                                                      \
   do {                                                                                         \
