@@ -19,6 +19,8 @@
 //   FH_EPI_SWIGLU   act = swiglu(bf16(gate), bf16(up)) in activation tile order
 //                   (gate/up tiles interleaved by the weight layout)
 //   FH_EPI_F32      out[m][n] = acc (FP32 logits)
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "../../include/ferric_hip.h"
@@ -144,24 +146,49 @@ constexpr int kBigTiles = 16;  // 16-row tiles per block side (256 rows)
 // each 8 n-tiles x 4 m-tiles (wave grid 2 along n x 4 along m). Only the
 // weight tiles go through LDS: each k-block's 16 weight tiles are fetched
 // global -> LDS directly (global_load_lds_dwordx4: lane i's 16 bytes land at
-// tile + 16 i, the tile-order layout itself), 2 per wave, into a 4-stage
-// ring. Every wave loads its own 4 activation tiles straight into registers
-// (a 3-slot ring; a tile is used by the 2 waves along n, so it is fetched
-// twice, the second time from the cache). Per k-block a workgroup reads
+// tile + 16 i, the tile-order layout itself), 2 per wave, into an
+// (LW + 1)-stage ring. Every wave loads its own 4 activation tiles straight
+// into registers (an (LX + 1)-slot ring; a tile is used by the 2 waves along
+// n, so it is fetched twice, the second time from the cache). Per k-block a
+// workgroup reads
 // 64 KiB out of LDS and writes 16 KiB; sharing the activation tiles through
 // LDS as well (96 KiB read, 32 KiB written, the kernel this replaced) made
 // LDS the bound, and this form is 14-28 % faster on the 8B projections with
 // bit-identical results. Barriers are bare s_barrier: __syncthreads()' fence
 // would wait for every load in flight, k-blocks ahead included.
+//
+// Counters on the gate/up projection (8192 x 24576 x 4096): 100.7M MFMAs of
+// 16 cycles keep the MFMA pipe busy 62 % of the kernel's cycles with no LDS
+// bank conflicts; the library GEMM reaches 85 % on the same shape but at a
+// lower clock under the board's power limit, about 10 % faster in time.
 constexpr unsigned xd_wait_vm(unsigned n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
 
-template <int EPI>
+// Calls f(std::integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// LX / LW: how many k-blocks ahead the activation / weight tiles are
+// requested (LW >= LX, so W(kb) is always older than X(kb)). Measured on the
+// 8B projections at m = 8192: LX = 3, LW = 4 is 2-7 % faster than 2 / 3
+// (212 VGPRs, 80 KiB LDS, still 2 waves per SIMD); deeper rings, reading all
+// of a k-block's weight tiles out of LDS up front, and two k-blocks per
+// barrier were not faster.
+template <int EPI, int LX = 3, int LW = 4>
 __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __restrict__ xt,
                                                             const uint16_t* __restrict__ w, uint32_t m,
                                                             uint32_t mtiles, uint32_t kb_count,
                                                             const uint16_t* residual, void* out, uint32_t ldo,
                                                             uint32_t out_mtiles) {
-  constexpr int WN = 8, WM = 4, WSTAGES = 4, XSLOTS = 3;
+  static_assert(LX >= 1 && LW >= LX, "weights requested no later than activations");
+  constexpr int WN = 8, WM = 4, WSTAGES = LW + 1, XSLOTS = LX + 1;
+  // Loads issued after X(kb): 2 weight and WM activation loads per later k-block.
+  constexpr unsigned kInFlight = (2 + WM) * (LX - 1);
+  static_assert(kInFlight < 64, "vmcnt range");
   __shared__ u32x4 wlds[WSTAGES][kBigTiles][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -179,15 +206,15 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
                                        (__attribute__((address_space(3))) void*)&wlds[kb % WSTAGES][2 * wave + t][0],
                                        16, 0, 0);
   };
-  // Activation tiles of this wave: (kb, bm + wm * WM + j).
+  // Activation tiles of this wave: (kb, bm + wm * WM + j), into register slot S.
   const u32x4* xsrc = reinterpret_cast<const u32x4*>(xt) + (uint64_t)(bm + wm * WM) * 64 + lane;
   const uint64_t x_kb = (uint64_t)mtiles * 64;
   u32x4 xr[XSLOTS][WM];
-#define FH_XD_LOADX(KB, SLOT)                                                                  \
-  do {                                                                                         \
-    const uint64_t k_ = min((uint32_t)(KB), last);                                             \
-    _Pragma("unroll") for (int j = 0; j < WM; ++j) xr[SLOT][j] = xsrc[k_ * x_kb + j * 64];      \
-  } while (0)
+  auto load_x = [&](auto slot_c, uint32_t kb) {
+    const uint64_t k = min(kb, last);
+#pragma unroll
+    for (int j = 0; j < WM; ++j) xr[decltype(slot_c)::value][j] = xsrc[k * x_kb + j * 64];
+  };
 
   f32x4 acc[WN][WM];
 #pragma unroll
@@ -195,42 +222,40 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
 #pragma unroll
     for (int j = 0; j < WM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Issue order per iteration j: W(j + 3), then X(j + 2). At iteration kb,
-  // X(kb) was issued two iterations back and W(kb + 2), X(kb + 1) after it:
-  // 2 + 4 = 6 loads may stay in flight. The prologue issues in the same
-  // order (W0 W1 X0 W2 X1), so the first iteration's wait covers X0 as well;
-  // with W2 after X0 the compiler had to add its own wait for X0 inside the
-  // loop, and with direct-to-LDS loads in flight that wait is vmcnt(0),
-  // which drained every load once per 3 k-blocks.
-  fetch_w(0);
-  fetch_w(1);
-  FH_XD_LOADX(0, 0);
-  fetch_w(2);
-  FH_XD_LOADX(1, 1);
-#define FH_XD_STEP(KB, S)                                                                      \
-  do {                                                                                         \
-    __builtin_amdgcn_s_waitcnt(xd_wait_vm(6));                                                 \
-    __builtin_amdgcn_s_barrier(); /* W(kb) of every wave is in LDS */                          \
-    fetch_w((KB) + 3);                                                                         \
-    FH_XD_LOADX((KB) + 2, ((S) + 2) % XSLOTS);                                                 \
-    const int st_ = (KB) % WSTAGES;                                                            \
-    _Pragma("unroll") for (int i = 0; i < WN; ++i) {                                           \
-      const u32x4 wv = wlds[st_][wn * WN + i][lane];                                           \
-      _Pragma("unroll") for (int j = 0; j < WM; ++j)                                           \
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(wv), b8(xr[S][j]), acc[i][j], 0, 0, 0); \
-    }                                                                                          \
-  } while (0)
+  // Issue order per iteration j: W(j + LW), then X(j + LX); k-blocks past
+  // the end are clamped to the last one, so the count of loads in flight is
+  // the same at every iteration. The prologue issues in that same order (for
+  // LX = 3, LW = 4: W0 W1 X0 W2 X1 W3 X2), so the first iteration's wait
+  // covers X0 as well. Issued in another order the compiler adds its own wait for X0
+  // inside the loop, and with direct-to-LDS loads in flight that wait is
+  // vmcnt(0), draining every load once per loop iteration.
+  static_for<0, LW>([&](auto j_c) {
+    constexpr int j = decltype(j_c)::value - LW;
+    fetch_w(j + LW);
+    if constexpr (j + LX >= 0) load_x(std::integral_constant<int, (j + LX) % XSLOTS>{}, j + LX);
+  });
+  auto step = [&](auto s_c, uint32_t kb) {
+    constexpr int S = decltype(s_c)::value;
+    __builtin_amdgcn_s_waitcnt(xd_wait_vm(kInFlight));
+    __builtin_amdgcn_s_barrier();  // W(kb) of every wave is in LDS
+    fetch_w(kb + LW);
+    load_x(std::integral_constant<int, (S + LX) % XSLOTS>{}, kb + LX);
+    const int st = kb % WSTAGES;
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      const u32x4 wv = wlds[st][wn * WN + i][lane];
+#pragma unroll
+      for (int j = 0; j < WM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b8(wv), b8(xr[S][j]), acc[i][j], 0, 0, 0);
+    }
+  };
   uint32_t kb = 0;
-  for (; kb + XSLOTS <= kb_count; kb += XSLOTS) {
-    FH_XD_STEP(kb, 0);
-    FH_XD_STEP(kb + 1, 1);
-    FH_XD_STEP(kb + 2, 2);
-  }
-  if (kb < kb_count) FH_XD_STEP(kb, 0);
-  if (kb + 1 < kb_count) FH_XD_STEP(kb + 1, 1);
+  for (; kb + XSLOTS <= kb_count; kb += XSLOTS)
+    static_for<0, XSLOTS>([&](auto s_c) { step(s_c, kb + decltype(s_c)::value); });
+  static_for<0, XSLOTS - 1>([&](auto s_c) {
+    if (kb + decltype(s_c)::value < kb_count) step(s_c, kb + decltype(s_c)::value);
+  });
   __builtin_amdgcn_s_waitcnt(xd_wait_vm(0));
-#undef FH_XD_STEP
-#undef FH_XD_LOADX
 
   const uint32_t nt0 = bn + wn * WN, mt0 = bm + wm * WM;
   if (mt0 * 16 >= m) return;  // this wave's rows are all padding
