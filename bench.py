@@ -87,12 +87,21 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 4}), flush=True)
 
 
+ATTN_PARTITION_TOKENS = 512  # 32 pages of 16 tokens per attention partition
+
+
 def kernel_bytes(cfg, rows, positions, stride):
     """Algorithmic HBM bytes per launch of each kernel class, for one step."""
     H, QH, KVH, I, V = cfg["hidden"], cfg["query_heads"], cfg["kv_heads"], cfg["intermediate"], cfg["vocabulary"]
     Q, KV = QH * 128, KVH * 128
     nqkv = Q + 2 * KV
-    kv_read = int(np.sum(np.asarray(positions, np.int64) + 1)) * KV * 2 * 2  # K and V rows, bf16
+    ctx = np.asarray(positions, np.int64) + 1
+    kv_read = int(np.sum(ctx)) * KV * 2 * 2  # K and V rows, bf16
+    # Rows longer than one 512-token partition leave one FP32 record
+    # (max, denominator, 128 numerators) per query head and partition.
+    parts = (ctx + ATTN_PARTITION_TOKENS - 1) // ATTN_PARTITION_TOKENS
+    merge_read = int(np.sum(np.where(parts > 1, parts, 0))) * QH * 130 * 4
+    merged_rows = int(np.sum(parts > 1))
     return {
         "attention": kv_read + rows * Q * 2,
         "qkv_gemm": nqkv * H * 2 + rows * H * 2 + rows * nqkv * 2,
@@ -102,7 +111,7 @@ def kernel_bytes(cfg, rows, positions, stride):
         "head_gemm": V * H * 2 + rows * H * 2 + rows * V * 4,
         "rmsnorm": rows * H * 2 * 2 + H * 2,
         "qknorm_rope_kv": rows * nqkv * 2 + rows * Q * 2 + rows * 2 * KV * 2,
-        "attention_merge": 0,
+        "attention_merge": merge_read + merged_rows * Q * 2,
         "argmax": rows * V * 4,
         "embedding": rows * H * 2 * 2,
     }
