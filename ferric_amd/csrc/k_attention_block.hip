@@ -20,7 +20,13 @@
 //   online softmax per query vector: m' = max(m, page max),
 //   alpha = exp(m - m'), l = l alpha + sum exp(s - m'), n = n alpha + P V
 //   (the recurrence of the reference taken one page at a time, FP32);
-//   PV on VALU in FP32: lane l owns dims 2l, 2l+1 of the 16 vectors.
+//   P V on v_mfma_f32_16x16x16bf16_1k. The score tile leaves lane (g, j)
+//   holding P[vector j][keys 4 g .. 4 g + 3], which is that MFMA's A operand
+//   as it stands. P is FP32; it enters as two bf16 terms, hi = bf16(p) and
+//   lo = bf16(p - hi), whose sum is within 2^-17 p of p, and both products
+//   are accumulated in FP32 (V is bf16, so every product is exact). V goes
+//   through LDS transposed (dimension-major, two tokens per dword), so the B
+//   operand of a lane (keys 4 g .. 4 g + 3 of one dimension) is two dwords.
 // Finally out = bf16(n / l) for each valid row.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -32,17 +38,17 @@ namespace {
 constexpr uint32_t kScaleBitsB = 0x3db504f3u;  // f32 1/sqrt(128), paged_decode.rs:31-35
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float exp2_based(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+// V page in LDS, transposed: word [dim][pair] holds tokens 2 pair (low half)
+// and 2 pair + 1 (high half) of one dimension; 9 words per dimension (8 and
+// a pad) spread a wave's 64 stores over 16 banks.
+constexpr int kVtPitch = 9;
 
 template <int G>
-__global__ __launch_bounds__(256) void attn_block_kernel(
+__global__ __launch_bounds__(256, 4) void attn_block_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, const uint32_t* __restrict__ blocks,
     uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
@@ -63,8 +69,7 @@ __global__ __launch_bounds__(256) void attn_block_kernel(
   const uint32_t* trow = table + (uint64_t)last * stride;
 
   __shared__ u32x4 ktile[2][16][17];
-  __shared__ u32x4 vtile[2][16][16];
-  __shared__ float pbuf[4][16][16];  // [wave][key][query vector]
+  __shared__ uint32_t vtile[2][128][kVtPitch];
 
   const int j = lane & 15, g16 = lane >> 4;
   const uint32_t rj = wave * kRowsPerWave + j / G;
@@ -89,33 +94,48 @@ __global__ __launch_bounds__(256) void attn_block_kernel(
     }
     return ph;
   };
-  // Loader mapping: thread t copies 16 bytes (dims 8 c .. 8 c + 7) of token
-  // t / 16 of the page, for K and for V.
+  // K loader: thread t copies 16 bytes (dims 8 c .. 8 c + 7) of token t / 16.
+  // V loader: wave w copies tokens 4 w .. 4 w + 3, one dword (dims 2 l,
+  // 2 l + 1) per lane and token: a whole 256-byte row per load.
   const uint32_t lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
-  auto src = [&](uint32_t ph) { return (((uint64_t)ph * 16 + lt) * kvh + h) * 128 + 8 * lc; };
+  auto ksrc = [&](uint32_t ph) { return (((uint64_t)ph * 16 + lt) * kvh + h) * 128 + 8 * lc; };
+  auto vsrc = [&](uint32_t ph, int t) {
+    return reinterpret_cast<const uint32_t*>(vc + (((uint64_t)ph * 16 + 4 * wave + t) * kvh + h) * 128) + lane;
+  };
   uint32_t ph_next = phys(1), ph_next2 = phys(2);
-  u32x4 kreg, vreg;
+  u32x4 kreg;
+  uint32_t vreg[4];
   {
-    const uint64_t o = src(phys(0));
-    kreg = *reinterpret_cast<const u32x4*>(kc + o);
-    vreg = *reinterpret_cast<const u32x4*>(vc + o);
+    const uint32_t ph0 = phys(0);
+    kreg = *reinterpret_cast<const u32x4*>(kc + ksrc(ph0));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph0, t);
   }
 
   const float scale = __builtin_bit_cast(float, kScaleBitsB);
   const float kNegInf = -__builtin_inff();
   float m_run = kNegInf, l_run = 0.f;
-  float acc[16][2];
+  // Output tiles, 16 dims each: lane l, element e holds vector 4 (l / 16) + e,
+  // dim 16 d + l % 16.
+  f32x4 acc[8];
 #pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v][0] = acc[v][1] = 0.f;
+  for (int d = 0; d < 8; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (uint32_t p = 0; p < npages; ++p) {
     const int b = p & 1;
     ktile[b][lt][lc] = kreg;
-    vtile[b][lt][lc] = vreg;
+    // Tokens (4 w, 4 w + 1) and (4 w + 2, 4 w + 3) -> pairs 2 w and 2 w + 1,
+    // for dims 2 l (low halves) and 2 l + 1 (high halves).
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      const uint32_t t0 = vreg[2 * pr], t1 = vreg[2 * pr + 1];
+      vtile[b][2 * lane][2 * wave + pr] = (t0 & 0xffffu) | (t1 << 16);
+      vtile[b][2 * lane + 1][2 * wave + pr] = (t0 >> 16) | (t1 & 0xffff0000u);
+    }
     if (p + 1 < npages) {
-      const uint64_t o = src(ph_next);
-      kreg = *reinterpret_cast<const u32x4*>(kc + o);
-      vreg = *reinterpret_cast<const u32x4*>(vc + o);
+      kreg = *reinterpret_cast<const u32x4*>(kc + ksrc(ph_next));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph_next, t);
     }
     ph_next = ph_next2;
     ph_next2 = phys(p + 3);
@@ -145,59 +165,58 @@ __global__ __launch_bounds__(256) void attn_block_kernel(
     const float m_new = fmaxf(m_run, pm);
     const float alpha = m_new == kNegInf ? 1.f : exp2_based(m_run - m_new);
     float ps = 0.f;
+    uint32_t hi[4], lo[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float pe = sv[e] > kNegInf ? exp2_based(sv[e] - m_new) : 0.f;
-      pbuf[wave][4 * g16 + e][j] = pe;
       ps += pe;
+      hi[e] = f32_to_bf16(pe);
+      lo[e] = f32_to_bf16(pe - bf16_to_f32(hi[e]));
     }
     ps += __shfl_xor(ps, 16, 64);
     ps += __shfl_xor(ps, 32, 64);
     l_run = l_run * alpha + ps;
     m_run = m_new;
-    wave_lds_sync();
+    const uint32_t a_hi[2] = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+    const uint32_t a_lo[2] = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+    const bf16x4 p_hi = __builtin_bit_cast(bf16x4, a_hi), p_lo = __builtin_bit_cast(bf16x4, a_lo);
 
-    // n = n alpha + P V over the page's 16 keys.
+    // n = n alpha + P V: row e of this lane's output tiles is vector
+    // 4 g16 + e, whose alpha lane 4 g16 + e computed.
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), v));
-      acc[v][0] *= a;
-      acc[v][1] *= a;
+    for (int e = 0; e < 4; ++e) {
+      const float a = __shfl(alpha, 4 * g16 + e, 64);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[d][e] *= a;
     }
-    const uint32_t* vt = reinterpret_cast<const uint32_t*>(&vtile[b][0][0]);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t w = vt[k * 64 + lane];
-      const float v0 = lo_bf16(w), v1 = hi_bf16(w);
-      const float4* pk = reinterpret_cast<const float4*>(&pbuf[wave][k][0]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float4 pq = pk[c];
-        acc[4 * c + 0][0] = fmaf(pq.x, v0, acc[4 * c + 0][0]);
-        acc[4 * c + 0][1] = fmaf(pq.x, v1, acc[4 * c + 0][1]);
-        acc[4 * c + 1][0] = fmaf(pq.y, v0, acc[4 * c + 1][0]);
-        acc[4 * c + 1][1] = fmaf(pq.y, v1, acc[4 * c + 1][1]);
-        acc[4 * c + 2][0] = fmaf(pq.z, v0, acc[4 * c + 2][0]);
-        acc[4 * c + 2][1] = fmaf(pq.z, v1, acc[4 * c + 2][1]);
-        acc[4 * c + 3][0] = fmaf(pq.w, v0, acc[4 * c + 3][0]);
-        acc[4 * c + 3][1] = fmaf(pq.w, v1, acc[4 * c + 3][1]);
-      }
+    for (int d = 0; d < 8; ++d) {
+      const uint32_t* vt = &vtile[b][16 * d + j][2 * g16];
+      const uint32_t bw[2] = {vt[0], vt[1]};
+      const bf16x4 vb = __builtin_bit_cast(bf16x4, bw);
+      acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_hi, vb, acc[d], 0, 0, 0);
+      acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_lo, vb, acc[d], 0, 0, 0);
     }
   }
 
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
+  for (int e = 0; e < 4; ++e) {
+    const int v = 4 * g16 + e;
+    const float L = __shfl(l_run, v, 64);
     const uint32_t rv = wave * kRowsPerWave + v / G;
     if (rv < nrows) {
-      const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), v));
-      const uint32_t o0 = f32_to_bf16(acc[v][0] / L), o1 = f32_to_bf16(acc[v][1] / L);
-      bad |= !(L > 0.f) | ((o0 & 0x7f80u) == 0x7f80u) | ((o1 & 0x7f80u) == 0x7f80u);
-      const uint32_t col = (h * G + v % G) * 128 + 2 * lane;
-      const uint32_t word = o0 | (o1 << 16);
-      if (out_mtiles)
-        *reinterpret_cast<uint32_t*>(out + act_offset_m(row0 + rv, col, out_mtiles)) = word;
-      else
-        reinterpret_cast<uint32_t*>(out + ((uint64_t)(row0 + rv) * qh + h * G + v % G) * 128)[lane] = word;
+      bad |= !(L > 0.f);
+      const uint32_t head = h * G + v % G;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint32_t o = f32_to_bf16(acc[d][e] / L);
+        bad |= (o & 0x7f80u) == 0x7f80u;
+        const uint32_t col = head * 128 + 16 * d + j;
+        if (out_mtiles)
+          out[act_offset_m(row0 + rv, col, out_mtiles)] = (uint16_t)o;
+        else
+          out[((uint64_t)(row0 + rv) * qh + head) * 128 + 16 * d + j] = (uint16_t)o;
+      }
     }
   }
   if (bad) raise_error(err, ERR_NONFINITE);
