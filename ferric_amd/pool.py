@@ -15,7 +15,7 @@ import random
 
 import numpy as np
 
-from .runner import PAGE_TOKENS, PagedLimits, PreparedBatch, PreparedRow
+from .runner import PAGE_TOKENS, PagedLimits, PreparedBatch, PreparedRow, PreparedRows
 
 
 class SequenceState:
@@ -69,29 +69,82 @@ class PagePool:
 
     def prepare(self, rows: list) -> PreparedBatch:
         """rows: [(sequence, token)] in scheduler order; consecutive rows of one
-        sequence take consecutive positions."""
-        pending: dict[int, int] = {}
-        prepared = []
-        for sid, token in rows:
-            st = self.sequences[sid]
-            pos = st.length + pending.get(sid, 0)
-            pending[sid] = pending.get(sid, 0) + 1
-            self._ensure(st, pos + 1)
-            prepared.append((sid, int(token), pos, int(st.pages[pos // PAGE_TOKENS])))
-        # Every row of a sequence sees the sequence's full reserved page list
-        # (a read-only copy: later growth of the sequence does not change it).
-        tables = {}
-        for sid in pending:
-            t = self.sequences[sid].pages.copy()
-            t.flags.writeable = False
-            tables[sid] = t
-        prepared = [PreparedRow(sid, token, pos, tables[sid], page) for sid, token, pos, page in prepared]
+        sequence take consecutive positions. Pages are reserved in row order
+        (a row whose position starts a page the sequence does not have yet
+        takes the next free page). Every row of a sequence sees the
+        sequence's full reserved page list, as a read-only snapshot."""
+        if len(rows) <= 256:
+            cols = self._prepare_loop(rows)
+        else:
+            cols = self._prepare_vector(rows)
+        states, sid, token, pos, group = cols
+        lens = np.array([st._count for st in states], dtype=np.int64)
+        offs = np.zeros(len(states), dtype=np.int64)
+        if len(states) > 1:
+            offs[1:] = np.cumsum(lens[:-1])
+        tables = np.concatenate([st.pages for st in states]) if states else np.zeros(0, np.uint32)
+        writable = tables[offs[group] + pos // PAGE_TOKENS] if len(token) else np.zeros(0, np.uint32)
+        prepared = PreparedRows(sid, token, pos, writable, tables, offs, lens, group)
         bid = self._next_batch
         self._next_batch += 1
         return PreparedBatch(bid, prepared, self.limits)
 
+    def _prepare_loop(self, rows: list):
+        group_of: dict[int, int] = {}
+        states, pending = [], []
+        sid, token, pos, group = [], [], [], []
+        for s, t in rows:
+            g = group_of.get(s)
+            if g is None:
+                g = group_of[s] = len(states)
+                states.append(self.sequences[s])
+                pending.append(0)
+            st = states[g]
+            p = st.length + pending[g]
+            pending[g] += 1
+            if p // PAGE_TOKENS >= st._count:
+                self._ensure(st, p + 1)
+            sid.append(s)
+            token.append(int(t))
+            pos.append(p)
+            group.append(g)
+        return (states, np.array(sid, dtype=np.int64), np.array(token, dtype=np.int64),
+                np.array(pos, dtype=np.int64), np.array(group, dtype=np.int64))
+
+    def _prepare_vector(self, rows: list):
+        n = len(rows)
+        sid = np.fromiter((r[0] for r in rows), dtype=np.int64, count=n)
+        token = np.fromiter((int(r[1]) for r in rows), dtype=np.int64, count=n)
+        # Sequences in order of first appearance; rank of each row within its
+        # sequence gives positions length, length + 1, ...
+        order = np.argsort(sid, kind="stable")
+        uniq, first, counts = np.unique(sid[order], return_index=True, return_counts=True)
+        appear = np.argsort(order[first], kind="stable")  # unique ids by first row
+        remap = np.empty(len(uniq), dtype=np.int64)
+        remap[appear] = np.arange(len(uniq), dtype=np.int64)
+        rank = np.empty(n, dtype=np.int64)
+        rank[order] = np.arange(n, dtype=np.int64) - np.repeat(first, counts)
+        group = np.empty(n, dtype=np.int64)
+        group[order] = np.repeat(remap, counts)
+        states = [self.sequences[int(u)] for u in uniq[appear]]  # KeyError for an unknown sequence
+        lengths = np.array([st.length for st in states], dtype=np.int64)
+        pos = lengths[group] + rank
+        # Page reservations happen at the rows that first need a page: the
+        # first row of a sequence, or a row entering a page not reserved yet.
+        have = np.array([st._count for st in states], dtype=np.int64)
+        event = (pos // PAGE_TOKENS >= have[group]) & ((rank == 0) | (pos % PAGE_TOKENS == 0))
+        for i in np.nonzero(event)[0]:
+            self._ensure(states[group[i]], int(pos[i]) + 1)
+        return states, sid, token, pos, group
+
     def commit(self, batch: PreparedBatch) -> None:
-        for r in batch.rows:
+        rows = batch.rows
+        if isinstance(rows, PreparedRows):
+            for s, p in zip(rows.sequence.tolist(), rows.position.tolist()):
+                st = self.sequences[s]
+                st.length = max(st.length, p + 1)
+            return
+        for r in rows:
             st = self.sequences[r.sequence]
             st.length = max(st.length, r.position + 1)
 

@@ -13,6 +13,7 @@ libferric_hip.so behind the C ABI; this module only marshals.
 from __future__ import annotations
 
 import ctypes
+from collections.abc import Sequence as _SequenceABC
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -54,6 +55,51 @@ class PreparedRow:
         return self.position % PAGE_TOKENS
 
 
+class PreparedRows(_SequenceABC):
+    """The rows of a prepared batch as columns: one entry per row for the
+    sequence, token, position and writable page, plus one page list per
+    sequence, all of them in one read-only uint32 buffer (`tables`, list g
+    at `table_offset[g]`, `table_len[g]` entries) that the sequence's rows
+    share (`table_index` picks the list). Indexing or iterating yields
+    PreparedRow objects, so it reads like a list of rows; the runner hands
+    the columns to the C ABI without a per-row loop."""
+
+    def __init__(self, sequence, token, position, writable, tables, table_offset, table_len, table_index):
+        token = np.asarray(token)
+        if token.size and (token.min() < 0 or token.max() > 0xFFFFFFFF):
+            raise ValueError("token outside u32")
+        self.sequence = np.asarray(sequence, dtype=np.uint64)
+        self.token = token.astype(np.uint32)
+        self.position = np.asarray(position, dtype=np.uint32)
+        self.writable = np.asarray(writable, dtype=np.uint32)
+        self.tables = np.ascontiguousarray(tables, dtype=np.uint32)
+        self.tables.flags.writeable = False
+        self.table_offset = np.asarray(table_offset, dtype=np.int64)
+        self.table_len = np.asarray(table_len, dtype=np.int64)
+        self.table_index = np.asarray(table_index, dtype=np.int64)
+
+    def __len__(self) -> int:
+        return len(self.token)
+
+    def _row(self, i: int) -> PreparedRow:
+        g = self.table_index[i]
+        off = int(self.table_offset[g])
+        return PreparedRow(int(self.sequence[i]), int(self.token[i]), int(self.position[i]),
+                           self.tables[off:off + int(self.table_len[g])], int(self.writable[i]))
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return [self._row(j) for j in range(*i.indices(len(self)))]
+        if i < 0:
+            i += len(self)
+        if not 0 <= i < len(self):
+            raise IndexError("row index out of range")
+        return self._row(i)
+
+    def __iter__(self):
+        return (self._row(i) for i in range(len(self)))
+
+
 @dataclass
 class PreparedBatch:
     """Move-only batch metadata (EngineeringTpPreparedBatchV1)."""
@@ -86,17 +132,33 @@ def _rows_to_c(rows: Sequence[PreparedRow]):
     n = len(rows)
     rec = np.zeros(max(n, 1), dtype=ROW_DTYPE)
     keep = [rec]
+    if isinstance(rows, PreparedRows):
+        keep.append(rows.tables)
+        if n:
+            base = rows.tables.ctypes.data if len(rows.tables) else 0
+            lens = rows.table_len[rows.table_index]
+            rec["sequence"][:n] = rows.sequence
+            rec["token"][:n] = rows.token
+            rec["position"][:n] = rows.position
+            rec["pages"][:n] = np.where(lens > 0, base + 4 * rows.table_offset[rows.table_index], 0).astype(np.uint64)
+            rec["page_count"][:n] = lens
+            rec["writable_page"][:n] = rows.writable
+        return ctypes.cast(rec.ctypes.data, ctypes.POINTER(_lib.Row)), keep
     seq, tok, pos, ptrs, cnt, wp = [], [], [], [], [], []
+    converted = {}  # id(page list) -> (array, pointer): rows of a sequence share one list
     for r in rows:
         pages = r.physical_pages
-        if not (isinstance(pages, np.ndarray) and pages.dtype == np.uint32 and pages.flags.c_contiguous):
-            pages = np.ascontiguousarray(np.asarray(pages, dtype=np.uint32))
-        keep.append(pages)
+        hit = converted.get(id(pages))
+        if hit is None or hit[2] is not pages:
+            arr = _page_array(pages)
+            hit = (arr, arr.ctypes.data if len(arr) else 0, pages)
+            converted[id(pages)] = hit
+            keep.append(arr)
         seq.append(r.sequence)
         tok.append(r.token)
         pos.append(r.position)
-        ptrs.append(pages.ctypes.data if len(pages) else 0)
-        cnt.append(len(pages))
+        ptrs.append(hit[1])
+        cnt.append(len(hit[0]))
         wp.append(r.writable_physical_page)
     if n:
         rec["sequence"][:n] = seq
@@ -106,6 +168,12 @@ def _rows_to_c(rows: Sequence[PreparedRow]):
         rec["page_count"][:n] = cnt
         rec["writable_page"][:n] = wp
     return ctypes.cast(rec.ctypes.data, ctypes.POINTER(_lib.Row)), keep
+
+
+def _page_array(pages) -> np.ndarray:
+    if isinstance(pages, np.ndarray) and pages.dtype == np.uint32 and pages.flags.c_contiguous:
+        return pages
+    return np.ascontiguousarray(np.asarray(pages, dtype=np.uint32))
 
 
 class TpBatchRunner:

@@ -153,6 +153,40 @@ def test_page_pool_reserves_write_slots_and_consecutive_positions():
         pool.prepare([(a, 1)] * 120)
 
 
+def test_page_pool_large_batch_matches_row_loop():
+    # Batches above 256 rows are prepared with array operations; they must
+    # give the same positions, page lists, write slots and page-allocation
+    # order as the row-by-row path, for interleaved sequences with prefixes.
+    from ferric_amd.runner import PreparedRows
+
+    limits = PagedLimits(context_tokens=1024, physical_page_count=400, page_table_stride=64)
+
+    def build():
+        pool = PagePool(limits, seed=11)
+        sids = [pool.admit(n) for n in (0, 15, 16, 33, 300)]
+        rng = np.random.default_rng(5)
+        rows = [(sids[i], int(t)) for i, t in zip(rng.integers(0, 5, 600), rng.integers(0, 151936, 600))]
+        return pool, rows
+
+    pool_a, rows = build()
+    pool_b, _ = build()
+    cols_a = pool_a._prepare_vector(rows)
+    cols_b = pool_b._prepare_loop(rows)
+    assert [st.sequence for st in cols_a[0]] == [st.sequence for st in cols_b[0]]
+    for x, y in zip(cols_a[1:], cols_b[1:]):
+        np.testing.assert_array_equal(x, y)
+    assert pool_a.free == pool_b.free
+    for s in pool_a.sequences:
+        np.testing.assert_array_equal(pool_a.sequences[s].pages, pool_b.sequences[s].pages)
+    batch = pool_a.prepare(rows[:400])
+    assert isinstance(batch.rows, PreparedRows) and len(batch.rows) == 400
+    r = batch.rows[-1]
+    assert r.writable_physical_page == r.physical_pages[r.position // 16]
+    assert not r.physical_pages.flags.writeable
+    with pytest.raises(ValueError):
+        pool_a.prepare([(rows[0][0], -1)] * 300)
+
+
 def test_library_shares_torch_hip_runtime():
     # Importing the package before torch must still leave one HIP runtime in
     # the process (two copies disagree about which devices exist).
