@@ -377,25 +377,28 @@ def main():
     setup_s = time.perf_counter() - t_setup
     print(f"# setup {setup_s:.1f} s: {name}, contexts mean {np.mean(contexts):.0f}", file=sys.stderr, flush=True)
 
+    outputs = list(range(batch))
+
     def step(toks):
         b = pool.prepare(list(zip(sids, toks)))
-        out = runner.execute_batch(b, list(range(batch)))
+        out = runner.execute_batch(b, outputs)
         pool.commit(b)
-        return out.choices, [r.position for r in b.rows]
+        return out.choices, b.rows.position  # the pool's prepared rows carry their columns
 
     for _ in range(args.warmup):
         tokens, _ = step(tokens)
 
-    step_byte_total = 0
+    step_positions = []
     device_ms = 0.0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tokens, positions = step(tokens)
         device_ms += runner.last_step_ms()
-        step_byte_total += step_bytes(cfg, batch, positions)
+        step_positions.append(positions)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    step_byte_total = sum(step_bytes(cfg, batch, p) for p in step_positions)
 
     # Per-kernel times: eager steps with an event pair around every launch.
     class_ms, class_launches, class_bytes = {}, {}, {}
