@@ -17,10 +17,35 @@ __host__ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
 }
 
-__host__ __device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+// The narrowing as integer operations on the bit pattern.
+__host__ __device__ __forceinline__ uint32_t f32_to_bf16_int(float v) {
   uint32_t b = __builtin_bit_cast(uint32_t, v);
   if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu) != 0u) return ((b >> 16) | 0x0040u) & 0xffffu;
   return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+// On the device this is gfx950's v_cvt_pk_bf16_f32 (what a __bf16 cast
+// compiles to): one instruction instead of the integer sequence, and equal to
+// it for all 2^32 inputs, NaN payloads included (compared exhaustively on an
+// MI355X).
+__host__ __device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)v);
+#else
+  return f32_to_bf16_int(v);
+#endif
+}
+
+// Two narrowings packed into one dword (lo in bits 0-15): one instruction on
+// the device.
+__host__ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+#else
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+#endif
 }
 
 // Value after a round trip through bf16 (the reference's intermediate narrowing).

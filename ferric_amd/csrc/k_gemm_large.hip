@@ -178,23 +178,43 @@ __device__ __forceinline__ void static_for(F&& f) {
 // (212 VGPRs, 80 KiB LDS, still 2 waves per SIMD); deeper rings, reading all
 // of a k-block's weight tiles out of LDS up front, and two k-blocks per
 // barrier were not faster.
+//
+// EPI == kEpiQkvRope (the QKV projection of a prefill chunk): a wave's 8
+// n-tiles are exactly one head (128 columns) of 64 rows. After the k loop the
+// wave stages them in LDS as bf16 rows (the projection's rounding) and lane r
+// runs the per-head QK-norm, RoPE and KV append of row r (qk_head.hpp): the
+// same lane code and order as the lane-per-head kernel, without the QKV
+// output's round trip through HBM or a second launch.
+constexpr int kEpiQkvRope = 16;
+constexpr int kQkPitch = 68;  // words per staged row: 64 + 4 keeps rows 16-byte aligned, reads conflict-free
+
 template <int EPI, int LX = 3, int LW = 4>
 __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __restrict__ xt,
                                                             const uint16_t* __restrict__ w, uint32_t m,
                                                             uint32_t mtiles, uint32_t kb_count,
                                                             const uint16_t* residual, void* out, uint32_t ldo,
-                                                            uint32_t out_mtiles) {
+                                                            uint32_t out_mtiles, const QkvRopeArgs qa) {
   static_assert(LX >= 1 && LW >= LX, "weights requested no later than activations");
   constexpr int WN = 8, WM = 4, WSTAGES = LW + 1, XSLOTS = LX + 1;
   // Loads issued after X(kb): 2 weight and WM activation loads per later k-block.
   constexpr unsigned kInFlight = (2 + WM) * (LX - 1);
   static_assert(kInFlight < 64, "vmcnt range");
-  __shared__ u32x4 wlds[WSTAGES][kBigTiles][64];
+  constexpr size_t kRingBytes = sizeof(u32x4) * WSTAGES * kBigTiles * 64;
+  constexpr size_t kStageBytes = EPI == kEpiQkvRope ? 4ull * 8 * 64 * kQkPitch : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kRingBytes > kStageBytes ? kRingBytes : kStageBytes];
+  auto& wlds = *reinterpret_cast<u32x4(*)[WSTAGES][kBigTiles][64]>(lds_raw);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t bn = blockIdx.x * kBigTiles, bm = blockIdx.y * kBigTiles;
   const int wn = wave % 2, wm = wave / 2;
   const uint32_t last = kb_count - 1;
+  // The fused QKV epilogue's row lookups (position, page, slot) are
+  // requested now and used after the k loop.
+  QkvRowSlot row_slot{0u, 0u, false};
+  if constexpr (EPI == kEpiQkvRope) {
+    const uint32_t row = (bm + wm * 4) * 16 + lane;
+    if (row < m) row_slot = qkv_row_slot(row, qa);
+  }
   // Weight fetch: tiles 2 wave, 2 wave + 1 of the block.
   const u32x4* wsrc = reinterpret_cast<const u32x4*>(w) + (uint64_t)(bn + 2 * wave) * kb_count * 64 + lane;
   const uint64_t w_tile = (uint64_t)kb_count * 64;
@@ -258,8 +278,31 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
   __builtin_amdgcn_s_waitcnt(xd_wait_vm(0));
 
   const uint32_t nt0 = bn + wn * WN, mt0 = bm + wm * WM;
-  if (mt0 * 16 >= m) return;  // this wave's rows are all padding
   const uint32_t q = lane >> 4, c = lane & 15;
+  if constexpr (EPI == kEpiQkvRope) {
+    __syncthreads();  // every wave is done reading the weight ring, which the staging reuses
+    if (mt0 * 16 >= m) return;  // this wave's rows are all padding
+    // D layout: lane l, element e holds column 16 i + 4 (l / 16) + e of the
+    // head and row 16 j + l % 16 of the wave's 64 rows.
+    uint32_t* rows_lds = reinterpret_cast<uint32_t*>(lds_raw) + (uint32_t)wave * 64 * kQkPitch;
+#pragma unroll
+    for (int j = 0; j < WM; ++j)
+#pragma unroll
+      for (int i = 0; i < WN; ++i) {
+        const uint2 v = make_uint2(f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16),
+                                   f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16));
+        *reinterpret_cast<uint2*>(rows_lds + (16 * j + c) * kQkPitch + 8 * i + 2 * q) = v;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t row = mt0 * 16 + lane;
+    if (row < m)
+      qknorm_rope_kv_head<32>(reinterpret_cast<const qk_u32x4*>(rows_lds + lane * kQkPitch), row,
+                              blockIdx.x * 2 + wn, qa, row_slot);
+    return;
+  }
+  if (mt0 * 16 >= m) return;  // this wave's rows are all padding
   if constexpr (EPI == FH_EPI_SWIGLU) {
     bool bad = false;
 #pragma unroll
@@ -307,6 +350,18 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
 
 }  // namespace
 
+hipError_t launch_gemm_qkv_rope(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                                const QkvRopeArgs& qa, hipStream_t s) {
+  const uint32_t mtiles = act_mtiles(m);
+  if (m <= kStreamedRows || n % (16 * kBigTiles) != 0 || k % 32 != 0 || mtiles % kBigTiles != 0 ||
+      n != (qa.qh + 2 * qa.kvh) * 128)
+    return hipErrorInvalidValue;
+  const dim3 grid(n / (16 * kBigTiles), mtiles / kBigTiles);
+  hipLaunchKernelGGL((gemm_large_xd_kernel<kEpiQkvRope>), grid, dim3(512), 0, s, x_tiled, w_tiled, m, mtiles, k / 32,
+                     (const uint16_t*)nullptr, (void*)nullptr, 0u, 0u, qa);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                              uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
   // Up to kStreamedRows rows the weight-streaming kernel is faster: it runs
@@ -321,7 +376,7 @@ hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, u
     const dim3 grid(n / (16 * kBigTiles), mtiles / kBigTiles);
 #define FH_BIG(E)                                                                                           \
   hipLaunchKernelGGL((gemm_large_xd_kernel<E>), grid, dim3(512), 0, s, x_tiled, w_tiled, m, mtiles, kb, residual, \
-                     out, ldo, out_mtiles)
+                     out, ldo, out_mtiles, QkvRopeArgs{})
     switch (epilogue) {
       case FH_EPI_BF16: FH_BIG(FH_EPI_BF16); break;
       case FH_EPI_RESIDUAL: FH_BIG(FH_EPI_RESIDUAL); break;

@@ -2,6 +2,7 @@
 // (one launch per layer), and the standalone K6 SwiGLU.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "qk_head.hpp"
 
 namespace fh {
 
@@ -19,23 +20,6 @@ __device__ __forceinline__ float block_sum_ordered(float v, float* red) {
 #pragma unroll
   for (int w = 1; w < kNormThreads / 64; ++w) t += red[w];
   return t;
-}
-
-// Inverse RMS exactly as qwen3_rmsnorm_v1 forms it
-// (device/qwen3-all-kernels-v1/src/rmsnorm.rs:440-456): mean = sum / width
-// (a division), + epsilon, correctly rounded sqrt, then 1 / sqrt.
-__device__ __forceinline__ float inverse_rms(float sum, float width, float eps) {
-  float mean_square = sum / width;
-  float stabilized = mean_square + eps;
-  float denominator = __fsqrt_rn(stabilized);
-  return __fdiv_rn(1.0f, denominator);
-}
-
-// Normalize-then-round, weight, round again (rmsnorm.rs:486-503; the witness
-// in device/qwen3-rmsnorm-v1/tests/reference.rs:264-274 pins the double round).
-__device__ __forceinline__ uint32_t norm_weight_bf16(float x, float inv, float w) {
-  float normalized = round_bf16(x * inv);
-  return f32_to_bf16(normalized * w);
 }
 
 // One workgroup per row; each thread owns 16-byte chunks c = tid, tid + 256, ...
@@ -320,106 +304,19 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
 }
 
 // The same computation for bf16 QKV rows (S = 0, the prefill path), one
-// lane per (row, head): the lane holds the head's 128 values and runs the
-// serial sum of squares (ascending element order, each square rounded
-// before the add, exactly as above) itself, so no cross-lane chain limits a
-// chunk of thousands of rows. Value heads are copied raw into the slot.
-__global__ __launch_bounds__(256, 2) void qknorm_rope_kv_rows_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const uint32_t* __restrict__ positions,
-    const uint32_t* __restrict__ table, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
-    uint32_t context, float eps, uint32_t* err) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const uint32_t all = qh + 2 * kvh;
+// lane per (row, head) (qk_head.hpp): the lane holds the head's 128 values
+// and runs the serial sum of squares (ascending element order, each square
+// rounded before the add, exactly as above) itself, so no cross-lane chain
+// limits a chunk of thousands of rows. Value heads are copied raw into the
+// slot.
+__global__ __launch_bounds__(256, 2) void qknorm_rope_kv_rows_kernel(const uint16_t* __restrict__ qkv, QkvRopeArgs a,
+                                                                     uint32_t rows) {
+  const uint32_t all = a.qh + 2 * a.kvh;
   const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (uint64_t)rows * all) return;
   const uint32_t row = (uint32_t)(gid / all), head = (uint32_t)(gid % all);
-  const u32x4* src = reinterpret_cast<const u32x4*>(qkv + (uint64_t)row * all * 128 + (uint64_t)head * 128);
-  uint32_t x[64];  // x[i] = elements 2 i (low half) and 2 i + 1 (high half)
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const u32x4 v = src[i];
-    x[4 * i] = v[0];
-    x[4 * i + 1] = v[1];
-    x[4 * i + 2] = v[2];
-    x[4 * i + 3] = v[3];
-  }
-  const uint32_t pos = positions[row];
-  uint32_t slot = 0;
-  bool slot_ok = pos < context && pos / 16 < stride;
-  if (slot_ok) {
-    const uint32_t page = table[(uint64_t)row * stride + pos / 16];
-    slot_ok = page < pages;
-    slot = (page * 16u + (pos & 15u)) * kvh;
-  }
-  if (!slot_ok && head == 0) raise_error(err, ERR_PAGE);
-  const uint32_t heads = qh + kvh;
-  if (head >= heads) {
-    if (slot_ok) {
-      u32x4* vo = reinterpret_cast<u32x4*>(v_cache + ((uint64_t)slot + (head - heads)) * 128);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) vo[i] = u32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
-    }
-    return;
-  }
-  // (A nonfinite element makes the sum nonfinite, which is checked.)
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float e0 = lo_bf16(x[i]), e1 = hi_bf16(x[i]);
-    const float s0 = e0 * e0, s1 = e1 * e1;
-    sum = sum + s0;
-    sum = sum + s1;
-  }
-  const float inv = inverse_rms(sum, 128.0f, eps);
-  bool bad = !is_finite_f32(sum) | !is_finite_f32(inv);
-  // Keep only the packed words live across the reduction (the unpacked
-  // values are recomputed), or the lane runs out of registers.
-#pragma unroll
-  for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(x[i]));
-  // Normalized in place, then rotated in place (pair words i and i + 32
-  // hold elements 2 i, 2 i + 1 and 2 i + 64, 2 i + 65).
-  const u32x4* wn = reinterpret_cast<const u32x4*>(head < qh ? q_norm : k_norm);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const u32x4 w = wn[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t xi = x[4 * i + j];
-      const uint32_t lo = norm_weight_bf16(lo_bf16(xi), inv, lo_bf16(w[j]));
-      const uint32_t hi = norm_weight_bf16(hi_bf16(xi), inv, hi_bf16(w[j]));
-      x[4 * i + j] = lo | (hi << 16);
-    }
-  }
-  const float* ct = cos_t + (uint64_t)(pos < context ? pos : 0) * 64;
-  const float* st = sin_t + (uint64_t)(pos < context ? pos : 0) * 64;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    if (i % 8 == 0) __builtin_amdgcn_sched_barrier(0);  // bounds how many cos/sin loads are hoisted
-    const float2 c = *reinterpret_cast<const float2*>(ct + 2 * i);
-    const float2 sn = *reinterpret_cast<const float2*>(st + 2 * i);
-    const float a0 = lo_bf16(x[i]), a1 = hi_bf16(x[i]);
-    const float b0 = lo_bf16(x[i + 32]), b1 = hi_bf16(x[i + 32]);
-    const float a0c = a0 * c.x, b0s = b0 * sn.x, b0c = b0 * c.x, a0s = a0 * sn.x;
-    const float a1c = a1 * c.y, b1s = b1 * sn.y, b1c = b1 * c.y, a1s = a1 * sn.y;
-    const uint32_t ra0 = f32_to_bf16(a0c - b0s), rb0 = f32_to_bf16(b0c + a0s);
-    const uint32_t ra1 = f32_to_bf16(a1c - b1s), rb1 = f32_to_bf16(b1c + a1s);
-    bad |= ((ra0 & 0x7f80u) == 0x7f80u) | ((rb0 & 0x7f80u) == 0x7f80u) | ((ra1 & 0x7f80u) == 0x7f80u) |
-           ((rb1 & 0x7f80u) == 0x7f80u);
-    x[i] = ra0 | (ra1 << 16);
-    x[i + 32] = rb0 | (rb1 << 16);
-  }
-  u32x4* dst = nullptr;
-  if (head < qh)
-    dst = reinterpret_cast<u32x4*>(q_out + ((uint64_t)row * qh + head) * 128);
-  else if (slot_ok)
-    dst = reinterpret_cast<u32x4*>(k_cache + ((uint64_t)slot + (head - qh)) * 128);
-  if (dst) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dst[i] = u32x4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
-  }
-  if (bad) raise_error(err, ERR_NONFINITE);
+  qknorm_rope_kv_head(reinterpret_cast<const qk_u32x4*>(qkv + (uint64_t)row * all * 128 + (uint64_t)head * 128), row,
+                      head, a, qkv_row_slot(row, a));
 }
 
 // RMSNorm of many rows into activation tile order (the prefill path, no
@@ -547,9 +444,9 @@ hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uin
                                  hipStream_t s) {
   if (!qkv_part) {
     const uint64_t lanes = (uint64_t)rows * (qh + 2 * kvh);
-    hipLaunchKernelGGL(qknorm_rope_kv_rows_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, qkv,
-                       q_norm, k_norm, cos_t, sin_t, positions, table, q_out, k_cache, v_cache, rows, qh, kvh, stride,
-                       pages, context, eps, err);
+    const QkvRopeArgs a{q_norm, k_norm, cos_t, sin_t, positions, table, q_out, k_cache, v_cache,
+                        qh,     kvh,    stride, pages, context, eps,   err};
+    hipLaunchKernelGGL(qknorm_rope_kv_rows_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, qkv, a, rows);
     return hipGetLastError();
   }
   const dim3 grid((qh + 2 * kvh + kHeadsPerGroup - 1) / kHeadsPerGroup, rows);

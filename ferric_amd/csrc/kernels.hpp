@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "qk_head.hpp"
+
 namespace fh {
 
 // Records the message fh_last_error(NULL) returns on this thread.
@@ -71,6 +73,13 @@ hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out
 // m > kMaxRows: no split-K; n % 128 == 0; x in activation tile order with act_mtiles(m) tiles.
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                              uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s);
+// The QKV projection of a prefill chunk with QK-norm, RoPE and the KV
+// append fused into its epilogue (qk_head.hpp), q written row-major to
+// qa.q_out. Only for the 256 x 256-block kernel: returns
+// hipErrorInvalidValue when m <= 256 or n % 256 != 0 (run the projection and
+// launch_qknorm_rope_kv instead).
+hipError_t launch_gemm_qkv_rope(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
+                                const QkvRopeArgs& qa, hipStream_t s);
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        hipStream_t s);

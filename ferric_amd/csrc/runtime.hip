@@ -877,6 +877,8 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     ++n;
   };
   const uint32_t R = nrows;
+  // The fused QKV epilogue needs the 256 x 256-block projection kernel.
+  const bool fused_qkv = R > 256 && ctx->nqkv % 256 == 0 && fh::act_mtiles(R) % 16 == 0;
   L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, p.hidden, R, H, V, err, s); });
   for (uint32_t l = 0; l < md.layers; ++l) {
@@ -886,13 +888,20 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     L(FH_KC_RMSNORM, [&] {
       return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.in_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
     });
-    L(FH_KC_QKV_GEMM, [&] {
-      return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, s);
-    });
-    L(FH_KC_QKNORM_ROPE_KV, [&] {
-      return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
-                                       p.qrot, kc, vc, R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
-    });
+    if (fused_qkv) {
+      // QK-norm, RoPE and the KV append run in the projection's epilogue.
+      const fh::QkvRopeArgs qa{W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, p.qrot, kc, vc,
+                               QH,       KVH,      stride,     pages,      C,     md.rms_epsilon, err};
+      L(FH_KC_QKV_GEMM, [&] { return fh::launch_gemm_qkv_rope(p.xn, W.qkv, R, ctx->nqkv, H, qa, s); });
+    } else {
+      L(FH_KC_QKV_GEMM, [&] {
+        return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, s);
+      });
+      L(FH_KC_QKNORM_ROPE_KV, [&] {
+        return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
+                                         p.qrot, kc, vc, R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
+      });
+    }
     L(FH_KC_ATTENTION, [&] {
       return fh::launch_attention_blocks(p.qrot, kc, vc, d_pos, d_tab, d_blocks, nblocks, p.attn, 1, R, QH, KVH,
                                          stride, pages, C, err, s);

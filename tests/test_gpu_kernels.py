@@ -287,6 +287,34 @@ def test_residual_rmsnorm(splits, rows, width):
     assert np.mean(got == ref) > 0.99
 
 
+def test_residual_narrowing_is_the_reference_rounding():
+    # hidden = bf16((0 + P) + 0) narrows arbitrary FP32 partials: ties to
+    # even, carries into the exponent, subnormals, overflow to infinity and
+    # NaN payloads (quieted, upper bits kept) must come out bit-exact
+    # (gemm reference.rs:112-135 vectors among them). Nonfinite outputs set
+    # the error word; the narrowed values are written either way.
+    special = [0x3f808000, 0x3f818000, 0x3f807fff, 0x3f808001, 0x3f7fffff, 0x7f7fffff, 0x7f7f7fff,
+               0x00008000, 0x00018000, 0x80008000, 0x807fffff, 0x7f800000, 0xff800000, 0x7fc00000,
+               0x7fa10001, 0xffa10001, 0x7f800001, 0x00000000, 0x80000000, 0x477fe000, 0xc77fe000]
+    width = 1024
+    bits = np.concatenate([np.array(special, np.uint32),
+                           rng(7).integers(0, 2**32, width - len(special), dtype=np.uint64).astype(np.uint32)])
+    slab = np.zeros((32, width), np.float32)
+    slab[0] = bits.view(np.float32)
+    hidden = np.zeros(width, np.uint16)
+    dh, dp = du.to_dev(hidden), du.to_dev(slab.reshape(-1))
+    dw_ = du.to_dev(np.full(width, 0x3f80, np.uint16))
+    dy = du.empty(tiled_rows(1) * width, np.uint16)
+    err = du.empty(1, np.uint32)
+    _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp), 1, du.ptr(dw_), du.ptr(dy), 1, 1, width, 1e-6,
+                                          du.ptr(err), du.stream()))
+    got = du.to_host(dh, np.uint16)
+    exp = orc.residual(slab[0].copy(), hidden)
+    assert np.array_equal(got, exp), [(hex(b), hex(g), hex(e)) for b, g, e in zip(bits, got, exp) if g != e][:8]
+    assert exp[0] == 0x3f80 and exp[1] == 0x3f82 and exp[14] == 0x7fe1  # the vectors' known answers
+    assert du.to_host(err, np.uint32)[0] != 0  # infinities and NaNs were seen
+
+
 def _paged_pool(r, pages, kvh, scale=1.0):
     n = pages * 16 * kvh * 128
     return rand_bf16(r, n, scale), rand_bf16(r, n, scale)

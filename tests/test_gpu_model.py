@@ -359,6 +359,15 @@ def test_prefill_chunk_8b_layer_shapes():
     _prefill_case(cfg, limits, [40], [100, 3000], 64, 37, "prefill 8b")
 
 
+def test_prefill_chunk_8b_fused_qkv_epilogue():
+    # 8B layer geometry, one layer, 292 rows: above 256 rows the QKV
+    # projection runs the 256 x 256-block kernel with QK-norm, RoPE and the KV
+    # append in its epilogue (32 query + 16 key/value heads, 24 column blocks).
+    cfg = dict(ferric_amd.QWEN3_8B, layers=1)
+    limits = PagedLimits(context_tokens=4096, physical_page_count=320, page_table_stride=256)
+    _prefill_case(cfg, limits, [150, 140], [100, 3000], 512, 43, "prefill 8b fused qkv")
+
+
 def test_prefill_continuation_and_interleaved_rows():
     # 0.6B shape, 2 layers. Prefill attention groups runs of rows of one
     # sequence at consecutive positions into blocks: a 70-row continuation of
