@@ -63,7 +63,27 @@ def build(verbose: bool = True) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY.relative_to(REPO_DIR)} from {len(sources)} sources", file=sys.stderr)
+    build_c_host(verbose)
     return LIBRARY
+
+
+C_HOST_SRC = REPO_DIR / "tests" / "c" / "abi_decode.c"
+C_HOST_BIN = REPO_DIR / "tests" / "c" / "abi_decode"
+
+
+def build_c_host(verbose: bool = True) -> Path:
+    """Compiles the plain-C host of the ABI (tests/c/abi_decode.c) with gcc
+    against the in-tree library (found at run time through its rpath)."""
+    rocm_lib = Path(HIPCC).resolve().parent.parent / "lib"
+    cmd = ["gcc", "-O2", "-std=c99", "-Wall", "-Wextra", "-I", str(REPO_DIR / "include"), str(C_HOST_SRC),
+           "-L", str(LIBRARY.parent), "-lferric_hip", f"-Wl,-rpath-link,{rocm_lib}",
+           "-Wl,-rpath,$ORIGIN/../../ferric_amd", "-o", str(C_HOST_BIN)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"gcc failed for {C_HOST_SRC.name}:\n{proc.stdout}\n{proc.stderr}")
+    if verbose:
+        print(f"built {C_HOST_BIN.relative_to(REPO_DIR)}", file=sys.stderr)
+    return C_HOST_BIN
 
 
 if __name__ == "__main__":
