@@ -220,6 +220,26 @@ def test_qwen3_8b_layer_shapes_match_oracle():
         pair.close()
 
 
+def test_qwen3_8b_full_depth_batch32_decode_step():
+    # The decode benchmark's shape at full size: Qwen3-8B with all 36 layers,
+    # batch 32, contexts U[512, 8192] on 16-token pages, through the HIP-graph
+    # path. Every layer and the head are held to their own error bars, the
+    # greedy choices to the oracle's end-to-end run.
+    cfg = dict(ferric_amd.QWEN3_8B)
+    rng = np.random.default_rng(2024)
+    lengths = [int(c) for c in rng.integers(512, 8193, 32)]
+    pages = sum(L // 16 + 2 for L in lengths) + 64
+    limits = PagedLimits(context_tokens=8208, physical_page_count=pages, page_table_stride=513)
+    pair = Pair(cfg, limits, seed=33, graphs=True, rows=32)
+    try:
+        sids = pair.admit_with_prefix(lengths)
+        toks = rng.integers(0, cfg["vocabulary"], len(sids))
+        batch, out, ref = pair.step(list(zip(sids, [int(t) for t in toks])))
+        pair.check(batch, out, ref, "8b full depth batch 32")
+    finally:
+        pair.close()
+
+
 def test_graph_replay_is_bit_identical_to_eager():
     cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
     limits = PagedLimits(context_tokens=512, physical_page_count=64, page_table_stride=32)
