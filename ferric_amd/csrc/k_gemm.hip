@@ -211,12 +211,22 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
 
 // Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
 // cold weights): weights of up to 16K rows use NT = 4 (activation traffic
-// half the weight traffic) with 8 waves; the fused gate/up weight (24K rows)
+// half the weight traffic) with 8 waves, or NT = 3 for split-K partials when
+// only that fills the CUs; the fused gate/up weight (24K rows)
 // keeps NT = 2 with 4 waves, twice as many workgroups in flight; the LM head
 // (152K rows) has n-tiles enough for NT = 4 with 4 waves.
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+  if constexpr (EPI == FH_EPI_PARTIAL) {
+    // Three n-tiles per wave where that puts exactly one workgroup on each
+    // of the 256 CUs and four would leave some idle (the 8B QKV weight:
+    // 6144 rows in 2 splits, 192 -> 256 workgroups, 11.4 -> 10.8 us).
+    if (n % 48 == 0 && n / 48 * splits == 256 && (n % 64 != 0 || n / 64 * splits < 256)) {
+      launch_variant<3, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+      return;
+    }
+  }
   if (n % 64 == 0 && n < 16384) {
     launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
   } else if (EPI != FH_EPI_SWIGLU && n % 64 == 0) {

@@ -213,7 +213,8 @@ def test_gemm_bf16_and_f32_epilogues(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(32, 6144, 4096, 6), (32, 4096, 12288, 8), (5, 1024, 1024, 2),
-                                          (17, 256, 4096, 3), (32, 64, 128, 4)])
+                                          (17, 256, 4096, 3), (32, 64, 128, 4),
+                                          (32, 6144, 4096, 2), (9, 6144, 1024, 2)])  # 3 n-tiles per wave
 def test_gemm_split_k_partials(m, n, k, splits):
     got, ref = _gemm_case(m, n, k, _lib.EPI_PARTIAL, 31 * m + splits, splits=splits)
     assert np.max(np.abs(got - ref)) <= F32_BOUND
