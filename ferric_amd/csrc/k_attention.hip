@@ -173,6 +173,9 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     // LDS tile (272-byte rows keep the column reads conflict-free).
     __shared__ u32x4 ktile[WAVES][16][17];
     u32x4 kr[kWavePages][4];
+    // Raised priority while the loads issue: the sequencer serves a wave
+    // that is issuing loads before other waves' ALU work, which keeps more
+    // bytes in flight (about 2.5 % on this kernel).
     __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (uint32_t u = 0; u < kWavePages; ++u) {
