@@ -173,10 +173,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     // LDS tile (272-byte rows keep the column reads conflict-free).
     __shared__ u32x4 ktile[WAVES][16][17];
     u32x4 kr[kWavePages][4];
-    // Raised priority while the loads issue: the sequencer serves a wave
-    // that is issuing loads before other waves' ALU work, which keeps more
-    // bytes in flight (about 2.5 % on this kernel).
-    __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (uint32_t u = 0; u < kWavePages; ++u) {
       if (u < np) {
@@ -186,7 +182,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
           kr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128));
       }
     }
-    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (uint32_t u = 0; u < kWavePages; ++u) {
       if (u < np) {
@@ -206,9 +201,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     }
   }
   // V loads go out now, so they are in flight during the softmax.
-  __builtin_amdgcn_s_setprio(3);
   load_v();
-  __builtin_amdgcn_s_setprio(0);
   pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
   pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
   float m[G], l[G], acc[G][2];
