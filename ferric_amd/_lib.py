@@ -122,7 +122,7 @@ SIGNATURES = [
     ("fh_op_untile_weight", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_embedding", _st, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     ("fh_op_rmsnorm", _st, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _vp, _vp]),
-    ("fh_op_gemm", _st, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    ("fh_op_gemm", _st, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp, _vp]),
     ("fh_gemm_default_splits", _u32, [_u32, _u32]),
     ("fh_activation_rows", _u32, [_u32]),
     ("fh_op_tile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
@@ -137,6 +137,8 @@ SIGNATURES = [
     ("fh_op_synth_fill", _st, [_vp, _u64, _u64, ctypes.c_float, _vp]),
     ("fh_speculative_token_assembly", _st, [_u32p, _u32p, _u32, _u32, _u32p]),
     ("fh_verify_greedy_round", _st, [_u32p, _u32, _u32p, _u32, _u32p, _u32p, _u32p]),
+    ("fh_compact_completion", _st, [_u32p, _u32p, _u32p, _u32p, _u32p, _u64p, ctypes.POINTER(ctypes.c_uint8), _u32,
+                                    _u32, _u32, ctypes.POINTER(ctypes.c_uint8)]),
 ]
 
 _lib = None

@@ -134,12 +134,30 @@ def read_header(path: str) -> tuple:
     return header, 8 + n
 
 
+def check_offset_coverage(path: str, ranges: list, data_bytes: int) -> None:
+    """The tensors of one shard, sorted by start offset, must tile its data
+    section exactly: no gap, no overlap, no trailing bytes (the reference's
+    validate_offset_coverage, crates/ferric-build/src/safetensors.rs:626-627,
+    762-790; header order itself is free)."""
+    expected = 0
+    for start, end, name in sorted(ranges):
+        if start > expected:
+            raise CheckpointError(f"{path}: offset gap before tensor {name!r} (expected {expected}, got {start})")
+        if start < expected:
+            raise CheckpointError(f"{path}: tensor {name!r} overlaps the previous one (expected {expected}, "
+                                  f"got {start})")
+        expected = end
+    if expected != data_bytes:
+        raise CheckpointError(f"{path}: tensors cover {expected} data bytes of {data_bytes} (trailing bytes)")
+
+
 def index_shards(cfg: Mapping, paths: Iterable[str]) -> list:
     """Parses and checks every shard header; returns the tensors to upload."""
     entries, seen = [], {}
     for path in paths:
         header, data0 = read_header(path)
         size = os.path.getsize(path)
+        ranges = []
         for name, spec in header.items():
             if name == "__metadata__":
                 continue
@@ -161,7 +179,9 @@ def index_shards(cfg: Mapping, paths: Iterable[str]) -> list:
             nbytes = 2 * int(np.prod(shape))
             if start < 0 or end - start != nbytes or data0 + end > size:
                 raise CheckpointError(f"tensor {name!r}: byte range does not match its shape")
+            ranges.append((start, end, name))
             entries.append(TensorEntry(name, kind, layer, shape, path, data0 + start, nbytes))
+        check_offset_coverage(path, ranges, size - data0)
     have = {(e.kind, e.layer) for e in entries}
     missing = required_tensors(cfg) - have
     if missing:

@@ -127,10 +127,8 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   // Physical pages of this wave, one per lane, read back with readlane so no
   // scalar table load sits between page loads.
   uint32_t my_phys = lane < (int)np ? raw_phys : 0u;
-  if (my_phys >= pages) {
-    bad = true;
-    my_phys = 0;
-  }
+  const bool bad_page = my_phys >= pages;  // an index fault, not a value fault
+  if (bad_page) my_phys = 0;
   auto phys_of = [&](uint32_t j) { return (uint32_t)__builtin_amdgcn_readlane((int)my_phys, (int)j); };
 
   // Pass 1: S^T = K Q^T on MFMA per page, scaled and masked scores to LDS,
@@ -323,6 +321,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     }
   }
   if (bad) raise_error(err, ERR_NONFINITE);
+  if (bad_page) raise_error(err, ERR_PAGE);
 }
 
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* __restrict__ part,

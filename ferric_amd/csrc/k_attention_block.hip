@@ -85,11 +85,11 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
     for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  bool bad = false;
+  bool bad = false, bad_page = false;
   auto phys = [&](uint32_t pi) {
     uint32_t ph = pi < npages ? trow[pi] : 0u;
     if (ph >= pages) {
-      bad = true;
+      bad_page = true;
       ph = 0;
     }
     return ph;
@@ -121,9 +121,19 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
 #pragma unroll
   for (int d = 0; d < 8; ++d) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Slots of the last page past the block's last position were never
+  // written by this sequence and may hold any bits; their P is 0, but 0 times
+  // a NaN or infinity inside the PV MFMA would still poison the sum, so they
+  // enter as zeros (the reference never reads past the row's position).
+  const uint32_t last_slot = pmax % 16;
   for (uint32_t p = 0; p < npages; ++p) {
     const int b = p & 1;
     ktile[b][lt][lc] = kreg;
+    if (p + 1 == npages) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if ((uint32_t)(4 * wave + t) > last_slot) vreg[t] = 0u;
+    }
     // Tokens (4 w, 4 w + 1) and (4 w + 2, 4 w + 3) -> pairs 2 w and 2 w + 1,
     // for dims 2 l (low halves) and 2 l + 1 (high halves).
 #pragma unroll
@@ -220,6 +230,7 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
     }
   }
   if (bad) raise_error(err, ERR_NONFINITE);
+  if (bad_page) raise_error(err, ERR_PAGE);
 }
 
 }  // namespace

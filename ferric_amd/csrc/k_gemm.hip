@@ -45,7 +45,8 @@ template <int NT, int MT, int EPI, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __restrict__ xt,
                                                          const uint16_t* __restrict__ w, uint32_t m_total,
                                                          uint32_t kb_count, uint32_t kb_split, uint32_t x_mtiles,
-                                                         const uint16_t* residual, void* out, uint32_t ldo) {
+                                                         const uint16_t* residual, void* out, uint32_t ldo,
+                                                         uint32_t* err) {
   __shared__ float red[WAVES][NT * MT * 256];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t tile0 = blockIdx.x * NT;
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
         reinterpret_cast<uint16_t*>(out)[act_offset_m(row0 + row, col, act_mtiles(m_total))] = (uint16_t)y;
       }
     }
-    (void)bad;  // a nonfinite activation surfaces at the next residual + norm
+    if (bad) raise_error(err, ERR_NONFINITE);
   } else {
     for (int idx = threadIdx.x; idx < NT * MT * 256; idx += WAVES * 64) {
       const int tm = idx >> 8, j = (idx >> 4) & 15, i = idx & 15;
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
 
 template <int NT, int EPI, int WAVES, int UNROLL>
 void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
-                    const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+                    const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
   const uint32_t kb = k / 32;
   const uint32_t kb_split = (kb + splits - 1) / splits;
   const uint32_t chunks = (m + 31) / 32;
@@ -203,10 +204,10 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
   const uint32_t x_mtiles = act_mtiles(m);
   if (m <= 16)
     hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       x_mtiles, residual, out, ldo);
+                       x_mtiles, residual, out, ldo, err);
   else
     hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       x_mtiles, residual, out, ldo);
+                       x_mtiles, residual, out, ldo, err);
 }
 
 // Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
@@ -217,24 +218,24 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
 // (152K rows) has n-tiles enough for NT = 4 with 4 waves.
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
-                const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+                const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
   if constexpr (EPI == FH_EPI_PARTIAL) {
     // Three n-tiles per wave where that puts exactly one workgroup on each
     // of the 256 CUs and four would leave some idle (the 8B QKV weight:
     // 6144 rows in 2 splits, 192 -> 256 workgroups, 11.4 -> 10.8 us).
     if (n % 48 == 0 && n / 48 * splits == 256 && (n % 64 != 0 || n / 64 * splits < 256)) {
-      launch_variant<3, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+      launch_variant<3, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
       return;
     }
   }
   if (n % 64 == 0 && n < 16384) {
-    launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
   } else if (EPI != FH_EPI_SWIGLU && n % 64 == 0) {
-    launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
   } else if (n % 32 == 0) {
-    launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
   } else if constexpr (EPI != FH_EPI_SWIGLU) {
-    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, s);
+    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
   }
 }
 
@@ -256,14 +257,14 @@ uint32_t gemm_default_splits(uint32_t n, uint32_t k) { return choose_splits(n, k
 
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
-                       hipStream_t s) {
+                       uint32_t* err, hipStream_t s) {
   if (splits == 0 || (m > kMaxRows && (splits != 1 || epilogue == FH_EPI_PARTIAL))) return hipErrorInvalidValue;
   switch (epilogue) {
-    case FH_EPI_BF16: launch_epi<FH_EPI_BF16>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
-    case FH_EPI_RESIDUAL: launch_epi<FH_EPI_RESIDUAL>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
-    case FH_EPI_SWIGLU: launch_epi<FH_EPI_SWIGLU>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
-    case FH_EPI_F32: launch_epi<FH_EPI_F32>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, s); break;
-    case FH_EPI_PARTIAL: launch_epi<FH_EPI_PARTIAL>(x_tiled, w_tiled, m, n, k, splits, residual, out, ldo, s); break;
+    case FH_EPI_BF16: launch_epi<FH_EPI_BF16>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;
+    case FH_EPI_RESIDUAL: launch_epi<FH_EPI_RESIDUAL>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;
+    case FH_EPI_SWIGLU: launch_epi<FH_EPI_SWIGLU>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;
+    case FH_EPI_F32: launch_epi<FH_EPI_F32>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;
+    case FH_EPI_PARTIAL: launch_epi<FH_EPI_PARTIAL>(x_tiled, w_tiled, m, n, k, splits, residual, out, ldo, err, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

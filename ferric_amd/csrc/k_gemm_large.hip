@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void gemm_large_kernel(const uint16_t* __restr
                                                          const uint16_t* __restrict__ w, uint32_t m,
                                                          uint32_t mtiles, uint32_t kb_count,
                                                          const uint16_t* residual, void* out, uint32_t ldo,
-                                                         uint32_t out_mtiles) {
+                                                         uint32_t out_mtiles, uint32_t* err) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t nt0 = blockIdx.x * kBlockTiles + (wave & 1) * kNT;  // first 16-row weight tile
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void gemm_large_kernel(const uint16_t* __restr
         *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + act_offset_m(row, col, out_mtiles)) = v;
       }
     }
-    (void)bad;  // a nonfinite activation surfaces at the next residual + norm
+    if (bad) raise_error(err, ERR_NONFINITE);
   } else {
 #pragma unroll
     for (int i = 0; i < kNT; ++i) {
@@ -193,7 +193,8 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w, uint32_t m,
                                                             uint32_t mtiles, uint32_t kb_count,
                                                             const uint16_t* residual, void* out, uint32_t ldo,
-                                                            uint32_t out_mtiles, const QkvRopeArgs qa) {
+                                                            uint32_t out_mtiles, const QkvRopeArgs qa,
+                                                            uint32_t* err) {
   static_assert(LX >= 1 && LW >= LX, "weights requested no later than activations");
   constexpr int WN = 8, WM = 4, WSTAGES = LW + 1, XSLOTS = LX + 1;
   // Loads issued after X(kb): 2 weight and WM activation loads per later k-block.
@@ -320,7 +321,7 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
         *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + act_offset_m(row, col, out_mtiles)) = v;
       }
     }
-    (void)bad;
+    if (bad) raise_error(err, ERR_NONFINITE);
   } else {
 #pragma unroll
     for (int i = 0; i < WN; ++i) {
@@ -358,16 +359,17 @@ hipError_t launch_gemm_qkv_rope(const uint16_t* x_tiled, const uint16_t* w_tiled
     return hipErrorInvalidValue;
   const dim3 grid(n / (16 * kBigTiles), mtiles / kBigTiles);
   hipLaunchKernelGGL((gemm_large_xd_kernel<kEpiQkvRope>), grid, dim3(512), 0, s, x_tiled, w_tiled, m, mtiles, k / 32,
-                     (const uint16_t*)nullptr, (void*)nullptr, 0u, 0u, qa);
+                     (const uint16_t*)nullptr, (void*)nullptr, 0u, 0u, qa, (uint32_t*)nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
-                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s) {
+                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err,
+                             hipStream_t s) {
   // Up to kStreamedRows rows the weight-streaming kernel is faster: it runs
   // 32-row chunks of the batch against the same weight tiles (a prefill
   // chunk of 17..32 rows when row_capacity < 32, a speculative verify batch).
-  if (m <= kStreamedRows) return launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, 1, residual, out, ldo, s);
+  if (m <= kStreamedRows) return launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, 1, residual, out, ldo, err, s);
   if (n % (16 * kBlockTiles) != 0 || k % 32 != 0) return hipErrorInvalidValue;
   const uint32_t mtiles = act_mtiles(m);
   const uint32_t out_mtiles = epilogue == FH_EPI_SWIGLU ? act_mtiles(m) : 0u;
@@ -376,7 +378,7 @@ hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, u
     const dim3 grid(n / (16 * kBigTiles), mtiles / kBigTiles);
 #define FH_BIG(E)                                                                                           \
   hipLaunchKernelGGL((gemm_large_xd_kernel<E>), grid, dim3(512), 0, s, x_tiled, w_tiled, m, mtiles, kb, residual, \
-                     out, ldo, out_mtiles, QkvRopeArgs{})
+                     out, ldo, out_mtiles, QkvRopeArgs{}, err)
     switch (epilogue) {
       case FH_EPI_BF16: FH_BIG(FH_EPI_BF16); break;
       case FH_EPI_RESIDUAL: FH_BIG(FH_EPI_RESIDUAL); break;
@@ -391,19 +393,19 @@ hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, u
   switch (epilogue) {
     case FH_EPI_BF16:
       hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_BF16>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
-                         residual, out, ldo, out_mtiles);
+                         residual, out, ldo, out_mtiles, err);
       break;
     case FH_EPI_RESIDUAL:
       hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_RESIDUAL>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
-                         residual, out, ldo, out_mtiles);
+                         residual, out, ldo, out_mtiles, err);
       break;
     case FH_EPI_SWIGLU:
       hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_SWIGLU>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
-                         residual, out, ldo, out_mtiles);
+                         residual, out, ldo, out_mtiles, err);
       break;
     case FH_EPI_F32:
       hipLaunchKernelGGL(gemm_large_kernel<FH_EPI_F32>, grid, dim3(256), 0, s, x_tiled, w_tiled, m, mtiles, kb,
-                         residual, out, ldo, out_mtiles);
+                         residual, out, ldo, out_mtiles, err);
       break;
     default:
       return hipErrorInvalidValue;

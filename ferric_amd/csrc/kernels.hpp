@@ -71,8 +71,10 @@ hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out
 
 // projections
 // m > kMaxRows: no split-K; n % 128 == 0; x in activation tile order with act_mtiles(m) tiles.
+// err receives ERR_NONFINITE from the SwiGLU epilogue (may be null).
 hipError_t launch_gemm_large(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
-                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, hipStream_t s);
+                             uint32_t epilogue, const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err,
+                             hipStream_t s);
 // The QKV projection of a prefill chunk with QK-norm, RoPE and the KV
 // append fused into its epilogue (qk_head.hpp), q written row-major to
 // qa.q_out. Only for the 256 x 256-block kernel: returns
@@ -82,7 +84,7 @@ hipError_t launch_gemm_qkv_rope(const uint16_t* x_tiled, const uint16_t* w_tiled
                                 const QkvRopeArgs& qa, hipStream_t s);
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
-                       hipStream_t s);
+                       uint32_t* err, hipStream_t s);
 uint32_t gemm_default_splits(uint32_t n, uint32_t k);
 
 // attention

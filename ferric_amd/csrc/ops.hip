@@ -62,7 +62,7 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
 
 fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                      uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
-                     void* stream) {
+                     uint32_t* error_word, void* stream) {
   if (!x_tiled || !w_tiled || !out || m == 0 || n == 0 || k == 0 || n % 16 || k % 32) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue > FH_EPI_PARTIAL || splits == 0 || splits > k / 32) return FH_ERR_INVALID_ARGUMENT;
   if (epilogue != FH_EPI_PARTIAL && splits != 1) return FH_ERR_INVALID_ARGUMENT;
@@ -76,9 +76,11 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
     // Prefill-size batches: 128 x 128 blocks, no split-K, 8-byte aligned rows.
     if (epilogue == FH_EPI_PARTIAL || n % (16 * 8) || (epilogue != FH_EPI_SWIGLU && ldo % 4))
       return FH_ERR_INVALID_ARGUMENT;
-    return from_hip(fh::launch_gemm_large(x_tiled, w_tiled, m, n, k, epilogue, residual, out, ldo, as_stream(stream)));
+    return from_hip(fh::launch_gemm_large(x_tiled, w_tiled, m, n, k, epilogue, residual, out, ldo, error_word,
+                                                  as_stream(stream)));
   }
-  return from_hip(fh::launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, splits, residual, out, ldo, as_stream(stream)));
+  return from_hip(fh::launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, splits, residual, out, ldo, error_word,
+                                            as_stream(stream)));
 }
 
 uint32_t fh_activation_rows(uint32_t m) { return m ? fh::act_mtiles(m) * 16 : 0u; }
@@ -177,6 +179,89 @@ fh_status fh_speculative_token_assembly(const uint32_t* anchors, const uint32_t*
     target_ids[(uint64_t)s * (k + 1)] = anchors[s];
     for (uint32_t i = 0; i < k; ++i) target_ids[(uint64_t)s * (k + 1) + 1 + i] = draft[(uint64_t)i * sequences + s];
   }
+  return FH_OK;
+}
+
+// Per-sequence completion record of ferric_qwen3_compact_completion_v1
+// (device/qwen3-all-kernels-v1/src/logits.rs:279-520), 120 bytes little-endian:
+//   [0,4) request slot  [4,8) request generation  [8,16) completion epoch
+//   [16,48) plan identity  [48] accepted  [49] emitted = accepted + 1  [50,52) 0
+//   [52,120) emitted tokens (draft[0..accepted) then the correction), then zeros.
+// A sequence with live length 0 gets an all-zero record and is not checked
+// further. The checks are the reference kernel's traps, in its order: live
+// <= active_tokens (and, speculative, live == active_tokens), slot < 32,
+// generation != 0, a nonzero plan identity, then each compared (draft, target)
+// pair below the vocabulary up to and including the first mismatch (tokens
+// after it are never read), then the correction token. The reference admits
+// a fixed profile table (logits.rs:293-304); this entry point accepts any
+// 1..32 sequences (its grid bound), active_tokens >= 1 and K <= 16 with
+// active_tokens = K + 1, which includes the 32-sequence K = 4 rounds the
+// reference's table stops short of. Nothing is written unless every
+// sequence passes.
+namespace {
+constexpr uint32_t kRecordBytes = 120;
+constexpr uint32_t kQwen3Vocabulary = 151936;  // QWEN3_LOGITS_VOCABULARY_V1, logits.rs:22
+constexpr uint32_t kMaxSpeculativeK = 16;       // QWEN3_LOGITS_MAX_SPECULATIVE_K_V1
+constexpr uint32_t kMaxSequences = 32;          // QWEN3_LOGITS_COMPACT_MAX_GRID_WORKGROUPS_V1
+
+void put_le(uint8_t* dst, uint64_t v, int bytes) {
+  for (int i = 0; i < bytes; ++i) dst[i] = (uint8_t)(v >> (8 * i));
+}
+
+bool one_record(const uint32_t* choices, const uint32_t* draft, uint32_t live, uint32_t slot, uint32_t generation,
+                uint64_t epoch, const uint8_t* plan, uint32_t sequences, uint32_t sequence, uint32_t active_tokens,
+                uint32_t k, uint8_t* rec) {
+  std::memset(rec, 0, kRecordBytes);
+  if (live == 0) return true;
+  if (live > active_tokens || (k != 0 && live != active_tokens)) return false;
+  if (slot >= 32 || generation == 0) return false;
+  bool plan_present = false;
+  for (int b = 0; b < 32; ++b) plan_present |= plan[b] != 0;
+  if (!plan_present) return false;
+  const uint64_t base = (uint64_t)sequence * active_tokens;
+  uint32_t accepted = 0;
+  while (accepted < k) {
+    const uint32_t d = draft[(uint64_t)accepted * sequences + sequence];
+    const uint32_t t = choices[base + accepted];
+    if (d >= kQwen3Vocabulary || t >= kQwen3Vocabulary) return false;
+    if (d != t) break;
+    ++accepted;
+  }
+  if (accepted >= active_tokens) return false;
+  const uint32_t correction = choices[base + (k == 0 ? live - 1 : accepted)];
+  if (correction >= kQwen3Vocabulary) return false;
+  put_le(rec + 0, slot, 4);
+  put_le(rec + 4, generation, 4);
+  put_le(rec + 8, epoch, 8);
+  std::memcpy(rec + 16, plan, 32);
+  rec[48] = (uint8_t)accepted;
+  rec[49] = (uint8_t)(accepted + 1);
+  for (uint32_t i = 0; i < accepted; ++i) put_le(rec + 52 + 4 * i, draft[(uint64_t)i * sequences + sequence], 4);
+  put_le(rec + 52 + 4 * accepted, correction, 4);
+  return true;
+}
+}  // namespace
+
+fh_status fh_compact_completion(const uint32_t* choices, const uint32_t* draft, const uint32_t* active_lengths,
+                                const uint32_t* request_slots, const uint32_t* request_generations,
+                                const uint64_t* completion_epochs, const uint8_t* plan_identities, uint32_t sequences,
+                                uint32_t active_tokens, uint32_t speculative_k, uint8_t* records) {
+  if (!choices || !active_lengths || !request_slots || !request_generations || !completion_epochs ||
+      !plan_identities || !records || sequences == 0 || sequences > kMaxSequences || active_tokens == 0 ||
+      speculative_k > kMaxSpeculativeK || (speculative_k != 0 && (!draft || active_tokens != speculative_k + 1))) {
+    fh::set_thread_error("compact completion: bad geometry");
+    return FH_ERR_INVALID_ARGUMENT;
+  }
+  uint8_t out[kMaxSequences * kRecordBytes];
+  for (uint32_t s = 0; s < sequences; ++s) {
+    if (!one_record(choices, draft, active_lengths[s], request_slots[s], request_generations[s],
+                    completion_epochs[s], plan_identities + 32ull * s, sequences, s, active_tokens, speculative_k,
+                    out + (uint64_t)s * kRecordBytes)) {
+      fh::set_thread_error("compact completion: a sequence's request, plan or tokens were rejected");
+      return FH_ERR_INVALID_ARGUMENT;
+    }
+  }
+  std::memcpy(records, out, (uint64_t)sequences * kRecordBytes);
   return FH_OK;
 }
 

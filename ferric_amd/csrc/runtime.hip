@@ -408,7 +408,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
       });
     L(FH_KC_QKV_GEMM, [&] {
       return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part, ctx->nqkv,
-                             s);
+                             err, s);
     });
     L(FH_KC_QKNORM_ROPE_KV, [&] {
       return fh::launch_qknorm_rope_kv(nullptr, ctx->qkv_part, sq, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos,
@@ -422,17 +422,17 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
       return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, 0, R, R, QH, C, err, s);
     });
     L(FH_KC_O_GEMM, [&] {
-      return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, s);
+      return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, err, s);
     });
     L(FH_KC_RMSNORM, [&] {
       return fh::launch_residual_rmsnorm(ctx->hidden, ctx->o_part, so, W.post_norm, ctx->xn, 1, R, H, md.rms_epsilon,
                                          err, s);
     });
     L(FH_KC_GATE_UP_GEMM, [&] {
-      return fh::launch_gemm(ctx->xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, 1, nullptr, ctx->act, I, s);
+      return fh::launch_gemm(ctx->xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, 1, nullptr, ctx->act, I, err, s);
     });
     L(FH_KC_DOWN_GEMM, [&] {
-      return fh::launch_gemm(ctx->act, W.down, R, H, I, FH_EPI_PARTIAL, sd, nullptr, ctx->down_part, H, s);
+      return fh::launch_gemm(ctx->act, W.down, R, H, I, FH_EPI_PARTIAL, sd, nullptr, ctx->down_part, H, err, s);
     });
   }
   L(FH_KC_RMSNORM, [&] {
@@ -445,7 +445,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
     });
   L(FH_KC_HEAD_GEMM, [&] {
     return fh::launch_gemm(ctx->xn, ctx->head, R, md.vocabulary, H, FH_EPI_F32, 1, nullptr, ctx->logits,
-                           md.vocabulary, s);
+                           md.vocabulary, err, s);
   });
   L(FH_KC_ARGMAX, [&] {
     return fh::launch_argmax(ctx->logits, R, md.vocabulary, ctx->argmax_scratch, ctx->choices, err, s);
@@ -895,7 +895,7 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
       L(FH_KC_QKV_GEMM, [&] { return fh::launch_gemm_qkv_rope(p.xn, W.qkv, R, ctx->nqkv, H, qa, s); });
     } else {
       L(FH_KC_QKV_GEMM, [&] {
-        return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, s);
+        return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, err, s);
       });
       L(FH_KC_QKNORM_ROPE_KV, [&] {
         return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
@@ -907,16 +907,16 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
                                          stride, pages, C, err, s);
     });
     L(FH_KC_O_GEMM, [&] {
-      return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);
+      return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
     });
     L(FH_KC_RMSNORM, [&] {
       return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.post_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
     });
     L(FH_KC_GATE_UP_GEMM, [&] {
-      return fh::launch_gemm_large(p.xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, p.act, I, s);
+      return fh::launch_gemm_large(p.xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, p.act, I, err, s);
     });
     L(FH_KC_DOWN_GEMM, [&] {
-      return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, s);
+      return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
     });
   }
   if (nout) {
@@ -927,8 +927,8 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     });
     L(FH_KC_HEAD_GEMM, [&] {
       return nout <= kMaxRows
-                 ? fh::launch_gemm(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, 1, nullptr, p.logits, V, s)
-                 : fh::launch_gemm_large(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, nullptr, p.logits, V, s);
+                 ? fh::launch_gemm(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, 1, nullptr, p.logits, V, err, s)
+                 : fh::launch_gemm_large(p.out_xn, ctx->head, nout, V, H, FH_EPI_F32, nullptr, p.logits, V, err, s);
     });
     L(FH_KC_ARGMAX, [&] { return fh::launch_argmax(p.logits, nout, V, p.argmax_scratch, p.choices, err, s); });
     ++n;  // argmax is two launches

@@ -19,13 +19,16 @@ either KV cache):
     When A == K the draft never consumed d[K-1]: the next round first runs
     a draft catch-up step with d[K-1] at position c + K.
 
-The integer work (assembly, settlement) runs through the C ABI
-(fh_speculative_token_assembly, fh_verify_greedy_round).
+The integer work (assembly, settlement, the per-sequence 120-byte
+completion record of ferric_qwen3_compact_completion_v1, logits.rs:279)
+runs through the C ABI (fh_speculative_token_assembly,
+fh_verify_greedy_round, fh_compact_completion).
 """
 
 from __future__ import annotations
 
 import ctypes
+import hashlib
 from dataclasses import dataclass
 
 import numpy as np
@@ -52,6 +55,7 @@ class RoundStats:
     draft_steps: int
     catch_up_rows: int
     target_rows: int
+    records: list = None  # one 120-byte completion record per sequence (bytes)
 
 
 def _u32(a):
@@ -84,18 +88,47 @@ def verify_greedy(draft, target):
     return int(acc.value), [int(x) for x in em[: n.value]]
 
 
+def compact_completion(choices, draft, active_lengths, slots, generations, epochs, plans, active_tokens, k):
+    """Per-sequence completion records (list of 120-byte strings) of
+    fh_compact_completion: choices [S][active_tokens], draft [K][S]
+    (iteration-major), plans: S 32-byte plan identities."""
+    lib = load()
+    s = len(active_lengths)
+    c, cp = _u32(np.asarray(choices, dtype=np.uint32).reshape(-1))
+    d, dp = _u32(np.asarray(draft, dtype=np.uint32).reshape(-1) if k else [0])
+    lv, lp = _u32(active_lengths)
+    sl, sp = _u32(slots)
+    gn, gp = _u32(generations)
+    ep = np.ascontiguousarray(np.asarray(epochs, dtype=np.uint64))
+    pl = np.frombuffer(b"".join(bytes(p) for p in plans), dtype=np.uint8).copy()
+    if pl.size != 32 * s:
+        raise ValueError("one 32-byte plan identity per sequence")
+    out = np.zeros(s * 120, dtype=np.uint8)
+    u8 = ctypes.POINTER(ctypes.c_uint8)
+    check(lib.fh_compact_completion(cp, dp if k else None, lp, sp, gp, ep.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                                    pl.ctypes.data_as(u8), s, active_tokens, k, out.ctypes.data_as(u8)))
+    return [bytes(out[i * 120:(i + 1) * 120]) for i in range(s)]
+
+
 class SpeculativeDecoder:
     """Greedy speculation of a draft runner for a target runner, each with
     its own KV pool. Sequences share prompts and cursors across the two."""
 
     def __init__(self, target: TpBatchRunner, target_pool: PagePool, draft: TpBatchRunner, draft_pool: PagePool,
-                 k: int = 4):
+                 k: int = 4, plan_identity: bytes = None):
         if k < 1:
             raise ValueError("a speculative round needs at least one draft token")
         self.target, self.tpool = target, target_pool
         self.draft, self.dpool = draft, draft_pool
         self.k = k
         self.seqs: list[SpecSequence] = []
+        # The 32-byte plan identity each completion record carries: the
+        # caller's, or a digest of this round's shape.
+        self.plan = plan_identity if plan_identity is not None else hashlib.sha256(
+            f"ferric-amd greedy speculative round K={k}".encode()).digest()
+        if len(self.plan) != 32:
+            raise ValueError("plan identity must be 32 bytes")
+        self.epoch = 0  # completion epoch: rounds settled so far
 
     def _run(self, runner, pool, rows, outputs):
         batch = pool.prepare(rows)
@@ -141,6 +174,14 @@ class SpeculativeDecoder:
         batch = self.tpool.prepare(rows)
         choices = np.asarray(self.target.execute_batch(batch, list(range(len(rows)))).choices,
                              dtype=np.uint32).reshape(len(seqs), k + 1)
+        # Completion records (slot = sequence index, generation 1, epoch = round),
+        # for at most the 32 request slots a record can name.
+        records = None
+        if len(seqs) <= 32:
+            n = len(seqs)
+            records = compact_completion(choices, draft, [k + 1] * n, list(range(n)), [1] * n, [self.epoch] * n,
+                                         [self.plan] * n, k + 1, k)
+        self.epoch += 1
         accepted, emitted = [], []
         for j, s in enumerate(seqs):
             a, em = verify_greedy(draft[:, j], choices[j])
@@ -154,4 +195,4 @@ class SpeculativeDecoder:
             s.emitted += em
             accepted.append(a)
             emitted.append(em)
-        return RoundStats(accepted, emitted, k, len(late), len(rows))
+        return RoundStats(accepted, emitted, k, len(late), len(rows), records)

@@ -226,10 +226,12 @@ enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3, 
 /* x_tiled is in activation tile order (fh_op_tile_activation). FH_EPI_SWIGLU writes its
  * output in activation tile order (the down projection's input); FH_EPI_PARTIAL writes
  * FP32 partial sums as `splits` slabs of [32][ldo] (split-K across workgroups; the
- * consumer adds the slabs in order and rounds once). Other epilogues use splits = 1. */
+ * consumer adds the slabs in order and rounds once). Other epilogues use splits = 1.
+ * error_word (may be NULL) receives the nonfinite bit where the SwiGLU epilogue meets a
+ * nonfinite gate, up or product (qwen3_swiglu_bf16_f32_v1 traps there). */
 fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                      uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
-                     void* stream);
+                     uint32_t* error_word, void* stream);
 /* Split-K factor the runtime uses for an n x k projection. */
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k);
 /* Rows a tiled activation buffer for m rows holds: 32 for m <= 32, else m rounded up to 256. */
@@ -301,6 +303,23 @@ fh_status fh_speculative_token_assembly(const uint32_t* anchors, const uint32_t*
 fh_status fh_verify_greedy_round(const uint32_t* draft, uint32_t draft_count, const uint32_t* target,
                                  uint32_t target_count, uint32_t* accepted, uint32_t* emitted,
                                  uint32_t* emitted_count);
+
+/* Per-sequence 120-byte completion records [sequences][120] of
+ * ferric_qwen3_compact_completion_v1 (device/qwen3-all-kernels-v1/src/logits.rs:279):
+ * slot u32 | generation u32 | epoch u64 | plan identity [32] | accepted u8 |
+ * emitted u8 | 0 0 | emitted tokens u32[17] (draft prefix, then the correction or
+ * bonus token; zeros after). choices: [sequences][active_tokens] (sequence-major);
+ * draft: [speculative_k][sequences] (iteration-major; NULL when speculative_k = 0,
+ * the direct profile, which emits the choice of the last live row). A sequence
+ * with active_lengths[s] = 0 gets an all-zero record. Returns
+ * FH_ERR_INVALID_ARGUMENT, writing nothing, where the reference kernel traps
+ * (live length, slot >= 32, generation 0, all-zero plan, a compared or emitted
+ * token >= 151936) or for bad geometry (1..32 sequences; speculative_k <= 16 with
+ * active_tokens = speculative_k + 1). Host-only: no device work. */
+fh_status fh_compact_completion(const uint32_t* choices, const uint32_t* draft, const uint32_t* active_lengths,
+                                const uint32_t* request_slots, const uint32_t* request_generations,
+                                const uint64_t* completion_epochs, const uint8_t* plan_identities, uint32_t sequences,
+                                uint32_t active_tokens, uint32_t speculative_k, uint8_t* records);
 
 #ifdef __cplusplus
 }

@@ -319,10 +319,29 @@ int orc_swiglu(const uint16_t* gate, const uint16_t* up, uint64_t count, uint16_
   return 0;
 }
 
-// TP1 residual (device/qwen3-tp-batch32-kernels-v5/src/collective.rs:25-60):
-// out = bf16((0 + partial) + residual).
-void orc_residual(const float* partial, const uint16_t* residual, uint64_t count, uint16_t* out) {
-  for (uint64_t i = 0; i < count; ++i) out[i] = narrow((0.0f + partial[i]) + widen(residual[i]));
+// TP1 residual (device/qwen3-tp-batch32-kernels-v5/src/collective.rs:5-60;
+// host-staged form adapters/m1-engineering-execution-v1/src/tp_execution/
+// collective.rs:44-66): out = bf16((0 + partial) + residual). The reference
+// rejects a nonfinite partial, a nonfinite partial sum, a nonfinite residual
+// or sum, and a sum whose bf16 rounding overflows. Every element is still
+// narrowed into out (the device path writes it too); rejected (may be NULL)
+// receives a per-element flag, and the return value is the number of
+// rejected elements (nonzero: the reference fails the batch).
+uint64_t orc_residual(const float* partial, const uint16_t* residual, uint64_t count, uint16_t* out,
+                      uint8_t* rejected) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < count; ++i) {
+    const float p = partial[i];
+    const float sum = 0.0f + p;
+    const float r = widen(residual[i]);
+    const float value = sum + r;
+    const uint16_t rounded = narrow(value);
+    out[i] = rounded;
+    const bool reject = !finite(p) || !finite(sum) || !finite(r) || !finite(value) || !finite_bf16(rounded);
+    if (rejected) rejected[i] = reject ? 1 : 0;
+    bad += reject ? 1 : 0;
+  }
+  return bad;
 }
 
 // Lowest-id argmax (logits.rs:197-270; v8 FP32 logits.rs:30): strict '>' scan.
@@ -386,6 +405,78 @@ int orc_verify_greedy(const uint32_t* draft, uint32_t draft_count, const uint32_
   *accepted = a;
   *emitted_count = a + 1;
   return 0;
+}
+
+// One sequence's compact completion record (ferric_qwen3_compact_completion_v1,
+// device/qwen3-all-kernels-v1/src/logits.rs:279-520), restating the reference's
+// test oracle compact_record_with_trace (device/qwen3-logits-v1/tests/reference.rs:
+// 106-191). Writes 120 bytes; returns 0, or 1 where that oracle returns None.
+// reads (may be NULL) receives the sequence of token reads, encoded as
+// (index << 1) | is_choice, and *nreads their count (at most 2 k + 1).
+int orc_compact_record(const uint32_t* choices, uint64_t nchoices, const uint32_t* draft, uint64_t ndraft,
+                       uint32_t live, uint32_t slot, uint32_t generation, uint64_t epoch, const uint8_t* plan,
+                       uint32_t sequences, uint32_t sequence, uint32_t active_tokens, uint32_t k, uint8_t* record,
+                       uint64_t* reads, uint32_t* nreads) {
+  const uint32_t kVocab = 151936;
+  uint32_t nr = 0;
+  auto note = [&](uint64_t index, bool choice) {
+    if (reads) reads[nr] = (index << 1) | (choice ? 1u : 0u);
+    ++nr;
+  };
+  int status = 1;
+  std::memset(record, 0, 120);
+  do {
+    if (live == 0) {
+      status = 0;
+      break;
+    }
+    const uint32_t direct_offset = live - 1;
+    bool plan_zero = true;
+    for (int b = 0; b < 32; ++b) plan_zero &= plan[b] == 0;
+    if (live > active_tokens || (k != 0 && live != active_tokens) || slot >= 32 || generation == 0 || plan_zero)
+      break;
+    const uint64_t choice_base = (uint64_t)sequence * active_tokens;
+    uint32_t accepted = 0;
+    bool fail = false;
+    if (k != 0) {
+      while (accepted < k) {
+        if (accepted >= k || sequence >= sequences) { fail = true; break; }
+        const uint64_t di = (uint64_t)accepted * sequences + sequence;
+        note(di, false);
+        if (di >= ndraft) { fail = true; break; }
+        const uint32_t d = draft[di];
+        if (sequence >= sequences || accepted >= active_tokens) { fail = true; break; }
+        const uint64_t ti = choice_base + accepted;
+        note(ti, true);
+        if (ti >= nchoices) { fail = true; break; }
+        const uint32_t t = choices[ti];
+        if (d >= kVocab || t >= kVocab) { fail = true; break; }
+        if (d != t) break;
+        ++accepted;
+      }
+    }
+    if (fail || accepted >= active_tokens) break;
+    const uint64_t ci = k == 0 ? choice_base + direct_offset : choice_base + accepted;
+    note(ci, true);
+    if (ci >= nchoices) break;
+    const uint32_t correction = choices[ci];
+    if (correction >= kVocab) break;
+    for (int i = 0; i < 4; ++i) record[i] = (uint8_t)(slot >> (8 * i));
+    for (int i = 0; i < 4; ++i) record[4 + i] = (uint8_t)(generation >> (8 * i));
+    for (int i = 0; i < 8; ++i) record[8 + i] = (uint8_t)(epoch >> (8 * i));
+    std::memcpy(record + 16, plan, 32);
+    record[48] = (uint8_t)accepted;
+    record[49] = (uint8_t)(accepted + 1);
+    for (uint32_t t = 0; t < accepted; ++t) {
+      const uint32_t v = draft[(uint64_t)t * sequences + sequence];
+      for (int i = 0; i < 4; ++i) record[52 + 4 * t + i] = (uint8_t)(v >> (8 * i));
+    }
+    for (int i = 0; i < 4; ++i) record[52 + 4 * accepted + i] = (uint8_t)(correction >> (8 * i));
+    status = 0;
+  } while (false);
+  if (status) std::memset(record, 0, 120);
+  if (nreads) *nreads = nr;
+  return status;
 }
 
 // ---- synthetic inputs (ferric_synth.h) ----
@@ -591,7 +682,7 @@ static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const 
   {
     std::vector<float> part((uint64_t)rows * H);
     orc_gemm(attn.data(), W.wo.data(), nullptr, rows, H, Q, 0, nullptr, part.data());
-    orc_residual(part.data(), h, (uint64_t)rows * H, h);
+    if (orc_residual(part.data(), h, (uint64_t)rows * H, h, nullptr)) return 1;
   }
   if (orc_rmsnorm(h, nullptr, W.post_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
   orc_gemm(xn.data(), W.wg.data(), nullptr, rows, I, H, 0, gate.data(), nullptr);
@@ -600,7 +691,7 @@ static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const 
   {
     std::vector<float> part((uint64_t)rows * H);
     orc_gemm(act.data(), W.wd.data(), nullptr, rows, H, I, 0, nullptr, part.data());
-    orc_residual(part.data(), h, (uint64_t)rows * H, h);
+    if (orc_residual(part.data(), h, (uint64_t)rows * H, h, nullptr)) return 1;
   }
   return 0;
 }

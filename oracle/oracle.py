@@ -66,7 +66,8 @@ def lib():
         L.orc_attention_head.restype = ctypes.c_int
         L.orc_swiglu.argtypes = [_u16p, _u16p, _c_u64, _u16p]
         L.orc_swiglu.restype = ctypes.c_int
-        L.orc_residual.argtypes = [_f32p, _u16p, _c_u64, _u16p]
+        L.orc_residual.argtypes = [_f32p, _u16p, _c_u64, _u16p, ctypes.POINTER(ctypes.c_uint8)]
+        L.orc_residual.restype = _c_u64
         L.orc_argmax_f32.argtypes = [_f32p, _c_u32, _f32p]
         L.orc_argmax_f32.restype = _c_u32
         L.orc_argmax_bf16.argtypes = [_u16p, _c_u32]
@@ -74,6 +75,10 @@ def lib():
         L.orc_token_assembly.argtypes = [_u32p, _u32p, _c_u32, _c_u32, _u32p]
         L.orc_verify_greedy.argtypes = [_u32p, _c_u32, _u32p, _c_u32, _u32p, _u32p, _u32p]
         L.orc_verify_greedy.restype = ctypes.c_int
+        L.orc_compact_record.argtypes = [_u32p, _c_u64, _u32p, _c_u64, _c_u32, _c_u32, _c_u32, _c_u64,
+                                         ctypes.POINTER(ctypes.c_uint8), _c_u32, _c_u32, _c_u32, _c_u32,
+                                         ctypes.POINTER(ctypes.c_uint8), _u64p, _u32p]
+        L.orc_compact_record.restype = ctypes.c_int
         L.orc_synth_fill.argtypes = [_u16p, _c_u64, _c_u64, ctypes.c_float]
         L.orc_splitmix64.argtypes = [_c_u64]
         L.orc_splitmix64.restype = _c_u64
@@ -221,12 +226,16 @@ def swiglu(gate, up):
     return None if st else out
 
 
-def residual(partial, res):
+def residual(partial, res, with_rejections=False):
+    """bf16((0 + partial) + res); with_rejections also returns the per-element
+    flags of the reference's rejections (nonfinite operands, sums or rounding)."""
     partial = np.ascontiguousarray(partial, dtype=np.float32)
     res = np.ascontiguousarray(res, dtype=np.uint16)
     out = np.zeros(len(res), np.uint16)
-    lib().orc_residual(_ptr(partial, _f32p), _ptr(res, _u16p), len(res), _ptr(out, _u16p))
-    return out
+    rej = np.zeros(len(res), np.uint8)
+    lib().orc_residual(_ptr(partial, _f32p), _ptr(res, _u16p), len(res), _ptr(out, _u16p),
+                       rej.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+    return (out, rej.astype(bool)) if with_rejections else out
 
 
 def argmax_f32(logits):
@@ -372,3 +381,21 @@ class Model:
         if want_hidden:
             out["hidden"] = hidden.reshape(d["layers"], rows, d["hidden"])
         return out
+
+
+def compact_record(choices, draft, live, slot, generation, epoch, plan, sequences, sequence, active_tokens, k):
+    """(record bytes or None, [("draft"|"choice", index) reads]) of one sequence,
+    as the reference's compact_record_with_trace."""
+    c = np.ascontiguousarray(np.asarray(choices, dtype=np.uint32).reshape(-1))
+    d = np.ascontiguousarray(np.asarray(draft, dtype=np.uint32).reshape(-1))
+    plan = np.frombuffer(bytes(plan), dtype=np.uint8).copy()
+    assert plan.size == 32
+    rec = np.zeros(120, np.uint8)
+    reads = np.zeros(2 * k + 2, np.uint64)
+    nr = np.zeros(1, np.uint32)
+    u8 = ctypes.POINTER(ctypes.c_uint8)
+    st = lib().orc_compact_record(_ptr(c, _u32p) if c.size else None, c.size, _ptr(d, _u32p) if d.size else None,
+                                  d.size, live, slot, generation, epoch, plan.ctypes.data_as(u8), sequences, sequence,
+                                  active_tokens, k, rec.ctypes.data_as(u8), _ptr(reads, _u64p), _ptr(nr, _u32p))
+    trace = [("choice" if int(r) & 1 else "draft", int(r) >> 1) for r in reads[: int(nr[0])]]
+    return (None if st else bytes(rec)), trace

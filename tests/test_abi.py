@@ -97,16 +97,16 @@ def test_scratch_sizes():
 def test_ops_reject_bad_shapes_before_any_launch():
     lib = ferric_amd.load()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    assert lib.fh_op_gemm(p, p, 0, 64, 64, 0, 1, None, p, 64, None) == 1  # m = 0
-    assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None) == 1  # m > 32 needs n % 128
-    assert lib.fh_op_gemm(p, p, 33, 128, 64, 4, 1, None, p, 128, None) == 1  # m > 32: no split-K partials
-    assert lib.fh_op_gemm(p, p, 33, 128, 64, 0, 1, None, p, 130, None) == 1  # m > 32: 8-byte aligned rows
-    assert lib.fh_op_gemm(p, p, 4, 60, 64, 0, 1, None, p, 64, None) == 1  # n % 16
-    assert lib.fh_op_gemm(p, p, 4, 64, 48, 0, 1, None, p, 64, None) == 1  # k % 32
-    assert lib.fh_op_gemm(p, p, 4, 64, 64, 1, 1, None, p, 64, None) == 1  # residual epilogue without residual
-    assert lib.fh_op_gemm(p, p, 4, 64, 64, 9, 1, None, p, 64, None) == 1  # unknown epilogue
-    assert lib.fh_op_gemm(p, p, 4, 64, 64, 0, 2, None, p, 64, None) == 1  # splits on a non-partial epilogue
-    assert lib.fh_op_gemm(p, p, 4, 64, 64, 4, 3, None, p, 64, None) == 1  # more splits than k-blocks
+    assert lib.fh_op_gemm(p, p, 0, 64, 64, 0, 1, None, p, 64, None, None) == 1  # m = 0
+    assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None, None) == 1  # m > 32 needs n % 128
+    assert lib.fh_op_gemm(p, p, 33, 128, 64, 4, 1, None, p, 128, None, None) == 1  # m > 32: no split-K partials
+    assert lib.fh_op_gemm(p, p, 33, 128, 64, 0, 1, None, p, 130, None, None) == 1  # m > 32: 8-byte aligned rows
+    assert lib.fh_op_gemm(p, p, 4, 60, 64, 0, 1, None, p, 64, None, None) == 1  # n % 16
+    assert lib.fh_op_gemm(p, p, 4, 64, 48, 0, 1, None, p, 64, None, None) == 1  # k % 32
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 1, 1, None, p, 64, None, None) == 1  # residual epilogue without residual
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 9, 1, None, p, 64, None, None) == 1  # unknown epilogue
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 0, 2, None, p, 64, None, None) == 1  # splits on a non-partial epilogue
+    assert lib.fh_op_gemm(p, p, 4, 64, 64, 4, 3, None, p, 64, None, None) == 1  # more splits than k-blocks
     assert lib.fh_op_tile_weight(p, p, 17, 32, None) == 1
     assert lib.fh_op_tile_activation(p, p, 33, 48, None) == 1  # k % 32
     assert lib.fh_activation_rows(1) == 32 and lib.fh_activation_rows(32) == 32

@@ -120,6 +120,53 @@ def test_rejections(tmp_path, case, match):
         load_safetensors(Recorder(TINY), paths)
 
 
+def _read_shard(path):
+    raw = open(path, "rb").read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    return json.loads(raw[8:8 + n]), raw[8 + n:]
+
+
+def _by_start(header):
+    return sorted((n for n in header if n != "__metadata__"), key=lambda n: header[n]["data_offsets"][0])
+
+
+@pytest.mark.parametrize("case,match", [
+    ("gap", "offset gap"),
+    ("overlap", "overlaps"),
+    ("trailing", "trailing"),
+])
+def test_offset_coverage_rejections(tmp_path, case, match):
+    # The reference's gaps_overlaps_invalid_ranges_and_reordering_are_rejected
+    # (crates/ferric-build/src/safetensors.rs:1305): the first tensor moved two
+    # bytes on (a gap at the start), the second tensor moved two bytes back (an
+    # overlap with the first), and two bytes past the last tensor.
+    paths = write_two_shards(tmp_path, make_tensors(TINY))
+    header, payload = _read_shard(paths[0])
+    first, second = _by_start(header)[:2]
+    if case == "gap":
+        header[first]["data_offsets"] = [o + 2 for o in header[first]["data_offsets"]]
+    elif case == "overlap":
+        header[second]["data_offsets"] = [o - 2 for o in header[second]["data_offsets"]]
+    else:
+        payload = payload + b"\0\0"
+    _raw_shard(paths[0], header, payload)
+    with pytest.raises(CheckpointError, match=match):
+        load_safetensors(Recorder(TINY), paths)
+
+
+def test_header_order_is_free(tmp_path):
+    # Coverage is checked over the tensors sorted by offset, so a header that
+    # lists them in another order admits the same bytes.
+    tensors = make_tensors(TINY)
+    paths = write_two_shards(tmp_path, tensors)
+    header, payload = _read_shard(paths[0])
+    _raw_shard(paths[0], dict(reversed(list(header.items()))), payload)
+    rec = Recorder(TINY)
+    load_safetensors(rec, paths)
+    for (kind, layer), got in rec.uploads.items():
+        assert np.array_equal(got, tensors[tensor_name(kind, layer)].reshape(-1))
+
+
 def test_duplicate_tensor_across_shards(tmp_path):
     tensors = make_tensors(TINY)
     paths = write_two_shards(tmp_path, tensors)

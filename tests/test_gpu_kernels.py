@@ -155,20 +155,30 @@ def test_activation_tile_order_round_trip():
         assert np.array_equal(du.to_host(back, np.uint16), x)
 
 
-def _gemm_case(m, n, k, epi, seed, splits=1):
+def _gemm_case(m, n, k, epi, seed, splits=1, poison_row=None):
+    """One fh_op_gemm launch against the oracle. poison_row: a NaN is planted
+    in that activation row (the SwiGLU epilogue must then raise the error word;
+    returns the error word instead of the outputs)."""
     r = rng(seed)
     x = rand_bf16(r, m * k, 1.0)
+    if poison_row is not None:
+        x[poison_row * k + 5] = 0x7FC0
     w = rand_bf16(r, n * k, 0.02)
     dxt = to_tiled_act(x, m, k)
     dw_ = du.to_dev(w)
     dt = du.empty(n * k, np.uint16)
+    err = du.empty(1, np.uint32)
     if epi == _lib.EPI_SWIGLU:
         i = n // 2
         gate, up = w[: i * k], w[i * k:]
         dg, du_ = du.to_dev(gate), du.to_dev(up)
         _lib.check(LIB.fh_op_tile_gate_up(du.ptr(dg), du.ptr(du_), du.ptr(dt), i, k, du.stream()))
         out_t = du.empty(tiled_rows(m) * i, np.uint16)  # activation tile order (the down projection's input)
-        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out_t), i, du.stream()))
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out_t), i, du.ptr(err),
+                                  du.stream()))
+        if poison_row is not None:
+            return int(du.to_host(err, np.uint32)[0])
+        assert du.to_host(err, np.uint32)[0] == 0
         out = du.empty(m * i, np.uint16)
         _lib.check(LIB.fh_op_untile_activation(du.ptr(out_t), du.ptr(out), m, i, du.stream()))
         got = du.to_host(out, np.uint16)
@@ -178,7 +188,7 @@ def _gemm_case(m, n, k, epi, seed, splits=1):
     _lib.check(LIB.fh_op_tile_weight(du.ptr(dw_), du.ptr(dt), n, k, du.stream()))
     if epi == _lib.EPI_PARTIAL:
         out = du.empty(splits * 32 * n, np.float32)
-        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, splits, None, du.ptr(out), n, du.stream()))
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, splits, None, du.ptr(out), n, None, du.stream()))
         slabs = du.to_host(out, np.float32).reshape(splits, 32, n)[:, :m]
         total = slabs[0].copy()
         for sp in range(1, splits):
@@ -186,16 +196,16 @@ def _gemm_case(m, n, k, epi, seed, splits=1):
         return total.reshape(-1), orc.gemm(x, w, m, n, k, f32_out=True)
     if epi == _lib.EPI_F32:
         out = du.empty(m * n, np.float32)
-        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, du.stream()))
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, None, du.stream()))
         return du.to_host(out, np.float32), orc.gemm(x, w, m, n, k, f32_out=True)
     if epi == _lib.EPI_RESIDUAL:
         res = rand_bf16(r, m * n, 1.0)
         out = du.to_dev(res)  # in place
-        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, du.ptr(out), du.ptr(out), n, du.stream()))
+        _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, du.ptr(out), du.ptr(out), n, None, du.stream()))
         part = orc.gemm(x, w, m, n, k, f32_out=True)
         return du.to_host(out, np.uint16), orc.residual(part, res)
     out = du.empty(m * n, np.uint16)
-    _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, du.stream()))
+    _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, 1, None, du.ptr(out), n, None, du.stream()))
     return du.to_host(out, np.uint16), orc.gemm(x, w, m, n, k)
 
 
@@ -232,6 +242,14 @@ def test_gemm_residual_and_swiglu_epilogues(m):
         # and SwiGLU multiplies them: <= 2 ulps of the product, plus exp's last ulp.
         assert du.bf16_close(got, ref, ulps=3)
         assert np.mean(got == ref) > 0.97
+
+
+@pytest.mark.parametrize("m", [3, 40, 300])  # decode kernel, 32-row chunks, 256 x 256 blocks
+def test_gemm_swiglu_epilogue_reports_nonfinite(m):
+    # A NaN in one activation row makes that row's gate and up NaN: the fused
+    # SwiGLU epilogue (decode and prefill kernels) raises the error word where
+    # qwen3_swiglu_bf16_f32_v1 traps (swiglu.rs:62-101).
+    assert _gemm_case(m, 256, 1024, _lib.EPI_SWIGLU, 5 + m, poison_row=m - 1) & 1
 
 
 @pytest.mark.parametrize("m", [33, 130, 257])
@@ -310,10 +328,11 @@ def test_residual_narrowing_is_the_reference_rounding():
     _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp), 1, du.ptr(dw_), du.ptr(dy), 1, 1, width, 1e-6,
                                           du.ptr(err), du.stream()))
     got = du.to_host(dh, np.uint16)
-    exp = orc.residual(slab[0].copy(), hidden)
+    exp, rejected = orc.residual(slab[0].copy(), hidden, with_rejections=True)
     assert np.array_equal(got, exp), [(hex(b), hex(g), hex(e)) for b, g, e in zip(bits, got, exp) if g != e][:8]
     assert exp[0] == 0x3f80 and exp[1] == 0x3f82 and exp[14] == 0x7fe1  # the vectors' known answers
-    assert du.to_host(err, np.uint32)[0] != 0  # infinities and NaNs were seen
+    assert rejected.any()
+    assert du.to_host(err, np.uint32)[0] != 0  # infinities and NaNs were seen, as the reference rejects
 
 
 def _paged_pool(r, pages, kvh, scale=1.0):
@@ -430,6 +449,26 @@ def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
                 # one key: softmax weight 1, output = V row bits exactly
                 assert np.array_equal(got[i, h], ref)
     assert worst <= 1e-2, worst
+
+
+def test_paged_attention_out_of_pool_page_is_a_page_error():
+    # A page-table entry past the pool is an index fault (the reference traps
+    # on it, paged_decode.rs:440-470): the error word carries the page bit, not
+    # the nonfinite bit, and the kernel reads nothing outside the pool.
+    r = rng(77)
+    qh, kvh, pages, stride, context = 32, 8, 64, 64, 1024
+    positions = np.array([700, 40, 5], np.uint32)
+    kc, vc = _paged_pool(r, pages, kvh)
+    q = rand_bf16(r, len(positions) * qh * 128, 1.0)
+    table = np.stack([r.permutation(pages)[:stride] for _ in positions]).astype(np.uint32)
+    table[0, 3] = pages + 5  # row 0 reads logical page 3
+    scratch = torch.zeros(LIB.fh_attention_scratch_bytes(3, qh, context) // 4, dtype=torch.float32, device="cuda")
+    out = du.empty(3 * qh * 128, np.uint16)
+    err = du.empty(1, np.uint32)
+    keep = [du.to_dev(a) for a in (q, kc, vc, positions, table)]
+    _lib.check(LIB.fh_op_paged_attention(*[du.ptr(t) for t in keep], du.ptr(out), 0, du.ptr(scratch), 3, qh, kvh,
+                                         stride, pages, context, du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 8  # ERR_PAGE only
 
 
 def test_paged_attention_long_context():

@@ -298,6 +298,32 @@ def test_residual_one_rounding_and_zero_partial():
     assert np.array_equal(got, exp)
 
 
+def test_residual_rejections():
+    # The reference rejects a nonfinite partial ("nonfinite row-parallel
+    # partial"), a nonfinite residual or sum ("nonfinite residual sum") and a
+    # finite sum whose bf16 rounding overflows ("BF16 residual sum overflow"):
+    # adapters/m1-engineering-execution-v1/src/tp_execution/collective.rs:44-66,
+    # v5 collective.rs:5-20. Finite cases next to them pass.
+    f32 = lambda b: np.array([b], np.uint32).view(np.float32)[0]  # noqa: E731
+    cases = [
+        (float("inf"), 0x3F80, True),          # nonfinite partial
+        (float("nan"), 0x0000, True),
+        (1.0, 0x7F80, True),                   # nonfinite residual
+        (1.0, 0x7FC0, True),
+        (f32(0x7F7FFFFF), 0x7F7F, True),       # sum overflows FP32
+        (f32(0x7F7FFFFF), 0x0000, True),       # finite sum, bf16 rounding overflows to inf
+        (f32(0x7F7F7FFF), 0x0000, False),      # largest sum that still rounds to a finite bf16
+        (-f32(0x7F7F7FFF), 0x8000, False),
+        (1.0, 0xBF80, False),                  # 1 + (-1) = 0
+    ]
+    parts = np.array([c[0] for c in cases], np.float32)
+    res = np.array([c[1] for c in cases], np.uint16)
+    out, rej = orc.residual(parts, res, with_rejections=True)
+    assert rej.tolist() == [c[2] for c in cases]
+    assert out[6] == 0x7F7F and out[7] == 0xFF7F and out[8] == 0x0000
+    assert out[5] == 0x7F80  # still narrowed (RNE carries into the infinity)
+
+
 # ---- argmax: device/qwen3-logits-v1/tests/reference.rs; v11 README.md:26-32 ----
 def test_argmax_lowest_id_rule():
     x = np.zeros(151936, np.float32)

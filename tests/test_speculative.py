@@ -126,3 +126,25 @@ def test_assembly_and_settlement_match_the_reference_vectors():
     assert verify_greedy([3, 4, 5], [9, 4, 5, 6]) == (0, [9])
     assert verify_greedy([3, 4, 5], [3, 4, 9, 6]) == (2, [3, 4, 9])
     assert verify_greedy([3, 4, 5], [3, 4, 5, 6]) == (3, [3, 4, 5, 6])
+
+
+def test_rounds_carry_compact_completion_records():
+    # Each round's 120-byte records (ferric_qwen3_compact_completion_v1,
+    # logits.rs:279) name the sequence's slot, the round's epoch and plan, and
+    # hold exactly the emitted tokens the settlement produced (the record
+    # builder itself is pinned to the reference's vectors in
+    # tests/test_compact_record.py).
+    import struct
+
+    dec, target, draft = make(4, 3)
+    dec.prefill([[1, 2, 3], [4, 5], [6]])
+    for epoch in range(5):
+        st = dec.round()
+        assert len(st.records) == 3
+        for s, rec in enumerate(st.records):
+            slot, gen, ep = struct.unpack_from("<IIQ", rec, 0)
+            assert (slot, gen, ep) == (s, 1, epoch) and rec[16:48] == dec.plan
+            a = st.accepted[s]
+            assert rec[48] == a and rec[49] == a + 1 == len(st.emitted[s])
+            assert list(struct.unpack_from(f"<{a + 1}I", rec, 52)) == st.emitted[s]
+            assert rec[52 + 4 * (a + 1):] == bytes(120 - 52 - 4 * (a + 1))
