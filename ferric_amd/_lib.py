@@ -108,6 +108,7 @@ SIGNATURES = [
     ("fh_kv_fill_synthetic", _st, [_vp, _u64, ctypes.c_float, ctypes.POINTER(Row), _u64p, _u32, _u32]),
     ("fh_read_kv_page", _st, [_vp, _u32, _u32, _u32, _u16p, _u64]),
     ("fh_write_kv_page", _st, [_vp, _u32, _u32, _u32, _u16p, _u64]),
+    ("fh_read_kv_cache", _st, [_vp, _u32, _u32, _u16p, _u64]),
     ("fh_execute_batch", _st, [_vp, _u64, ctypes.POINTER(Row), _u32, _u32p, _u32, _u32p]),
     ("fh_read_logits", _st, [_vp, _f32p, _u64]),
     ("fh_read_hidden", _st, [_vp, _u32, _u16p, _u64]),

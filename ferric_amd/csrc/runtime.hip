@@ -83,7 +83,8 @@ struct fh_ctx {
   void* argmax_scratch = nullptr;
   uint32_t* choices = nullptr;
   uint32_t* err = nullptr;
-  uint16_t* capture = nullptr;
+  uint16_t* capture = nullptr;  // [layers][capture_rows][hidden]: residual stream after each layer
+  uint32_t capture_rows = 0;    // max(row_capacity, prefill_rows)
 
   uint32_t* d_meta = nullptr;  // tokens[cap] | positions[cap] | table[cap][stride]
   uint32_t* h_meta = nullptr;  // pinned mirror
@@ -117,7 +118,8 @@ struct fh_ctx {
   uint64_t last_batch = 0;
   uint64_t dispatches = 0;
   uint64_t step_launches = 0;
-  uint32_t last_rows = 0;
+  uint32_t last_rows = 0;        // rows with logits in the last batch (output rows for prefill)
+  uint32_t last_batch_rows = 0;  // token rows of the last batch
   std::string error;
 
   std::map<uint32_t, hipGraphExec_t> graphs;
@@ -404,7 +406,8 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
     });
     if (ctx->capture && l > 0)
       L(FH_KC_RMSNORM, [&] {
-        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(l - 1) * cap * H, (uint64_t)R * H, s);
+        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(l - 1) * ctx->capture_rows * H,
+                                   (uint64_t)R * H, s);
       });
     L(FH_KC_QKV_GEMM, [&] {
       return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part, ctx->nqkv,
@@ -441,7 +444,8 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   });
   if (ctx->capture)
     L(FH_KC_RMSNORM, [&] {
-      return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(md.layers - 1) * cap * H, (uint64_t)R * H, s);
+      return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(md.layers - 1) * ctx->capture_rows * H,
+                                 (uint64_t)R * H, s);
     });
   L(FH_KC_HEAD_GEMM, [&] {
     return fh::launch_gemm(ctx->xn, ctx->head, R, md.vocabulary, H, FH_EPI_F32, 1, nullptr, ctx->logits,
@@ -574,7 +578,8 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&ctx->argmax_scratch), fh_argmax_scratch_bytes(cap)));
   TRY(dalloc(ctx, &ctx->choices, cap));
   TRY(dalloc(ctx, &ctx->err, 64));
-  if (op.capture_hidden) TRY(dalloc(ctx, &ctx->capture, (uint64_t)md.layers * cap * H));
+  ctx->capture_rows = std::max(cap, op.prefill_rows);
+  if (op.capture_hidden) TRY(dalloc(ctx, &ctx->capture, (uint64_t)md.layers * ctx->capture_rows * H));
   const uint64_t meta = 2ull * cap + (uint64_t)cap * op.page_table_stride;
   TRY(dalloc(ctx, &ctx->d_meta, meta));
   TRY(halloc(ctx, &ctx->h_meta, meta));
@@ -801,6 +806,14 @@ fh_status fh_read_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t 
   return FH_OK;
 }
 
+fh_status fh_read_kv_cache(fh_ctx* ctx, uint32_t layer, uint32_t which, uint16_t* out, uint64_t elements) {
+  if (!ctx || !out || layer >= ctx->md.layers || which > 1 || elements != ctx->kv_slab_elems)
+    return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad KV cache request");
+  FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  FH_HIP(ctx, hipMemcpy(out, kv_cache(ctx, layer, which), elements * 2, hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
 fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page, const uint16_t* data,
                            uint64_t elements) {
   if (!ctx || !data || layer >= ctx->md.layers || which > 1 || page >= ctx->opt.physical_pages ||
@@ -918,6 +931,10 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     L(FH_KC_DOWN_GEMM, [&] {
       return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
     });
+    if (ctx->capture)
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_copy_u16(p.hidden, ctx->capture + (uint64_t)l * ctx->capture_rows * H, (uint64_t)R * H, s);
+      });
   }
   if (nout) {
     L(FH_KC_RMSNORM, [&] { return fh::launch_gather_rows(p.hidden, d_out, p.out_hidden, nout, H, s); });
@@ -946,6 +963,7 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);
   if (ctx->profiling) collect_profile(ctx);
   ctx->last_rows = nout;
+  ctx->last_batch_rows = nrows;
   ctx->last_logits = p.logits;
   ctx->last_was_prefill = true;
   const uint32_t errw = p.h_out[kMaxPrefillOutputs];
@@ -1023,6 +1041,7 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);
   if (ctx->profiling) collect_profile(ctx);
   ctx->last_rows = nrows;
+  ctx->last_batch_rows = nrows;
   ctx->last_logits = ctx->logits;
   ctx->last_was_prefill = false;
   const uint32_t errw = ctx->h_out[cap];
@@ -1045,10 +1064,10 @@ fh_status fh_read_logits(fh_ctx* ctx, float* out, uint64_t elements) {
 }
 
 fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t elements) {
-  if (!ctx || !out || !ctx->capture || ctx->last_was_prefill || layer >= ctx->md.layers ||
-      elements > (uint64_t)ctx->last_rows * ctx->md.hidden)
+  if (!ctx || !out || !ctx->capture || layer >= ctx->md.layers ||
+      elements > (uint64_t)ctx->last_batch_rows * ctx->md.hidden)
     return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad hidden-state request (capture_hidden off?)");
-  FH_HIP(ctx, hipMemcpy(out, ctx->capture + (uint64_t)layer * ctx->opt.row_capacity * ctx->md.hidden, elements * 2,
+  FH_HIP(ctx, hipMemcpy(out, ctx->capture + (uint64_t)layer * ctx->capture_rows * ctx->md.hidden, elements * 2,
                         hipMemcpyDeviceToHost));
   return FH_OK;
 }

@@ -192,7 +192,8 @@ class TpBatchRunner:
         st = self._lib.fh_create(ctypes.byref(self._desc), ctypes.byref(self._opts), ctypes.byref(ctx))
         check(st, None, "fh_create")
         self._ctx = ctx
-        self._rows_last = 0
+        self._rows_last = 0  # rows with logits in the last batch
+        self._batch_rows_last = 0  # token rows of the last batch
 
     # ---- reference boundary ----
     def row_capacity(self) -> int:
@@ -211,6 +212,7 @@ class TpBatchRunner:
         check(st, self._ctx)
         # Decode batches produce logits for every row, prefill chunks for the output rows only.
         self._rows_last = len(batch.rows) if len(batch.rows) <= self._opts.row_capacity else len(outs)
+        self._batch_rows_last = len(batch.rows)
         return BatchOutput([int(c) for c in choices[: len(outs)]])
 
     def output_head_rows(self, physical: int, published: int) -> int:
@@ -266,17 +268,26 @@ class TpBatchRunner:
         return out.reshape(self._rows_last, self.model["vocabulary"])
 
     def read_hidden(self, layer: int) -> np.ndarray:
-        n = self._rows_last * self.model["hidden"]
+        """Residual stream after `layer` for every token row of the last batch."""
+        n = self._batch_rows_last * self.model["hidden"]
         out = np.zeros(n, dtype=np.uint16)
         check(self._lib.fh_read_hidden(self._ctx, layer, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n),
               self._ctx)
-        return out.reshape(self._rows_last, self.model["hidden"])
+        return out.reshape(self._batch_rows_last, self.model["hidden"])
 
     def read_kv_page(self, layer: int, which: int, page: int) -> np.ndarray:
         n = PAGE_TOKENS * self.model["kv_heads"] * 128
         out = np.zeros(n, dtype=np.uint16)
         check(self._lib.fh_read_kv_page(self._ctx, layer, which, page,
                                         out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n), self._ctx)
+        return out
+
+    def read_kv_cache(self, layer: int, which: int) -> np.ndarray:
+        """One layer's whole K (which = 0) or V (1) pool, [pages * 16 * kv_heads * 128] bf16."""
+        n = self.limits.physical_page_count * PAGE_TOKENS * self.model["kv_heads"] * 128
+        out = np.zeros(n, dtype=np.uint16)
+        check(self._lib.fh_read_kv_cache(self._ctx, layer, which, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                         n), self._ctx)
         return out
 
     def write_kv_page(self, layer: int, which: int, page: int, data: np.ndarray) -> None:

@@ -56,6 +56,8 @@ class RoundStats:
     catch_up_rows: int
     target_rows: int
     records: list = None  # one 120-byte completion record per sequence (bytes)
+    draft: np.ndarray = None  # the round's draft choices, iteration-major [K][S]
+    target_choices: np.ndarray = None  # the verify batch's choices [S][K + 1]
 
 
 def _u32(a):
@@ -195,4 +197,4 @@ class SpeculativeDecoder:
             s.emitted += em
             accepted.append(a)
             emitted.append(em)
-        return RoundStats(accepted, emitted, k, len(late), len(rows), records)
+        return RoundStats(accepted, emitted, k, len(late), len(rows), records, draft, choices)

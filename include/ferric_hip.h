@@ -139,6 +139,9 @@ fh_status fh_read_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t 
                           uint64_t elements);
 fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t page,
                            const uint16_t* data, uint64_t elements);
+/* Copies one layer's whole K or V pool ([physical_pages][16][kv_heads][head_dim] bf16;
+ * elements must be that size): a parity readback, like fh_read_kv_page. */
+fh_status fh_read_kv_cache(fh_ctx* ctx, uint32_t layer, uint32_t which, uint16_t* out, uint64_t elements);
 
 /* ---- the hot path ---- */
 
@@ -155,8 +158,10 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
 fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
                            const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out);
 
-/* Parity readbacks of the last batch: FP32 logits [nrows][vocabulary]; the
- * residual stream after layer `layer` [nrows][hidden] (needs capture_hidden). */
+/* Parity readbacks of the last batch: FP32 logits [nrows][vocabulary] (prefill: the
+ * output rows, in output order); the residual stream after layer `layer`
+ * [nrows][hidden] for every token row of the batch (needs capture_hidden, which
+ * holds max(row_capacity, prefill_rows) rows per layer). */
 fh_status fh_read_logits(fh_ctx* ctx, float* out, uint64_t elements);
 fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t elements);
 

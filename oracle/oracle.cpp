@@ -196,6 +196,120 @@ void orc_gemm_a4(const uint16_t* a, const uint16_t* b, const uint16_t* prior_c, 
     }
 }
 
+// ---- the reference's wave-order profiles (a second legal reduction order) ----
+// The serial functions above are the v1 semantics. The reference's resident
+// decode path reassociates the same sums across a 64-lane wave:
+//   * wave GEMV (device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15-137,
+//     partial form :142): lane l accumulates the products k = 64 s + l for
+//     s = 0, 1, ... in order, then reduce_sum_f32::<64> combines the lanes;
+//   * wave RMSNorm (device/qwen3-tp-wave-rmsnorm-kernels-v15/src/rmsnorm.rs:
+//     60-75): lane l accumulates x[l + 64 c]^2 for c = 0, 1, ..., then the
+//     same reduction;
+//   * wave attention (device/qwen3-tp-wave-query-hoist-kernels-v14/src/
+//     attention.rs:174-217): lane l forms q[l] k[l] + q[l+64] k[l+64], then
+//     the reduction gives the score; the online softmax is the serial one.
+// reduce_sum_f32::<64> is fe2o3's (not in the reference tree); it is taken
+// here as the xor butterfly v += lane(v ^ off) for off = 32, 16, ..., 1,
+// which leaves every lane with the same value because each addition is
+// commutative. These give the spread two legal orders of the reference's own
+// arithmetic produce end to end, the yardstick for a third order's (the
+// GPU's) drift.
+static float wave_reduce64(float* v) {
+  float t[64];
+  for (int off = 32; off > 0; off >>= 1) {
+    for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ off];
+    std::memcpy(v, t, sizeof(t));
+  }
+  return v[0];
+}
+
+// C = A W^T in wave-GEMV order (k % 64 == 0). out (bf16, one RNE) or out_f32.
+void orc_gemm_wave(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n, uint32_t k, uint16_t* out,
+                   float* out_f32) {
+  std::vector<float> af((uint64_t)m * k);
+  for (uint64_t i = 0; i < (uint64_t)m * k; ++i) af[i] = widen(a[i]);
+  const uint32_t steps = k / 64;
+#pragma omp parallel
+  {
+    std::vector<float> w(k);
+    float lanes[64];
+#pragma omp for schedule(static)
+    for (int64_t col = 0; col < (int64_t)n; ++col) {
+      const uint16_t* brow = b + (uint64_t)col * k;
+      for (uint32_t c = 0; c < k; ++c) w[c] = widen(brow[c]);
+      for (uint32_t r = 0; r < m; ++r) {
+        const float* ar = af.data() + (uint64_t)r * k;
+        for (int l = 0; l < 64; ++l) lanes[l] = 0.f;
+        for (uint32_t st = 0; st < steps; ++st) {
+          const float* as = ar + (uint64_t)st * 64;
+          const float* ws = w.data() + (uint64_t)st * 64;
+          for (int l = 0; l < 64; ++l) {
+            float product = as[l] * ws[l];
+            lanes[l] = lanes[l] + product;
+          }
+        }
+        const float sum = wave_reduce64(lanes);
+        const uint64_t o = (uint64_t)r * n + col;
+        if (out_f32)
+          out_f32[o] = sum;
+        else
+          out[o] = narrow(sum);
+      }
+    }
+  }
+}
+
+// Wave-order sum of squares of one row (width % 64 == 0): lane l adds
+// x[l + 64 c]^2 in ascending c, then the 64-lane butterfly.
+float orc_square_sum_wave(const uint16_t* x, uint32_t width) {
+  float lanes[64];
+  for (int l = 0; l < 64; ++l) {
+    float partial = 0.f;
+    for (uint32_t c = (uint32_t)l; c < width; c += 64) {
+      const float v = widen(x[c]);
+      const float sq = v * v;
+      partial = partial + sq;
+    }
+    lanes[l] = partial;
+  }
+  return wave_reduce64(lanes);
+}
+
+// Pure RMSNorm with the wave-order sum of squares (width % 64 == 0); the
+// normalize-and-weight step is the serial one. Returns 1 where the reference traps.
+int orc_rmsnorm_wave(const uint16_t* input, const uint16_t* weight, uint32_t rows, uint32_t width, float eps,
+                     uint16_t* norm_out) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint64_t base = (uint64_t)r * width;
+    float lanes[64];
+    for (int l = 0; l < 64; ++l) {
+      float partial = 0.f;
+      for (uint32_t c = (uint32_t)l; c < width; c += 64) {
+        const float x = widen(input[base + c]);
+        const float sq = x * x;
+        const float next = partial + sq;
+        if (!finite(x) || !finite(sq) || !finite(next)) return 1;
+        partial = next;
+      }
+      lanes[l] = partial;
+    }
+    const float sum = wave_reduce64(lanes);
+    const float mean_square = sum / (float)width;
+    const float stabilized = mean_square + eps;
+    const float denominator = std::sqrt(stabilized);
+    const float inverse = 1.0f / denominator;
+    if (!finite(sum) || !finite(mean_square) || !finite(stabilized) || stabilized <= 0.f || !finite(denominator) ||
+        denominator <= 0.f || !finite(inverse))
+      return 1;
+    for (uint32_t c = 0; c < width; ++c) {
+      const uint32_t o = orc_norm_weight(widen(input[base + c]) * inverse, weight[c]);
+      if (o == 0xffffffffu) return 1;
+      norm_out[base + c] = (uint16_t)o;
+    }
+  }
+  return 0;
+}
+
 // ferric_qwen3_token_embedding_bf16_copy_v1 (gemm.rs:768-853): bit copy;
 // returns the first row whose token is out of range + 1, or 0.
 uint32_t orc_embedding(const uint32_t* tokens, const uint16_t* weight, uint32_t rows, uint32_t hidden,
@@ -241,9 +355,28 @@ uint64_t orc_cache_index(uint32_t physical_page, uint32_t token_in_page, uint32_
 // (paged_decode.rs:222-572; device/qwen3-paged-decode-v1/tests/reference.rs:33-121):
 // keys 0..=position through `pages`, serial 128-wide dot, score * f32(0x3db504f3),
 // online softmax, out = bf16(n / l). Returns 1 where the reference traps.
+static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  const uint32_t* pages, uint32_t page_count, uint32_t physical_pages,
+                                  uint32_t position, uint32_t kv_heads, uint32_t kv_head, uint16_t* out, int order);
+
 int orc_attention_head(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* pages,
                        uint32_t page_count, uint32_t physical_pages, uint32_t position, uint32_t kv_heads,
                        uint32_t kv_head, uint16_t* out) {
+  return attention_head_ordered(q, k_cache, v_cache, pages, page_count, physical_pages, position, kv_heads, kv_head,
+                                out, 0);
+}
+
+// The same head with the score dot in wave order (v14 attention.rs:174-217).
+int orc_attention_head_wave(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                            const uint32_t* pages, uint32_t page_count, uint32_t physical_pages, uint32_t position,
+                            uint32_t kv_heads, uint32_t kv_head, uint16_t* out) {
+  return attention_head_ordered(q, k_cache, v_cache, pages, page_count, physical_pages, position, kv_heads, kv_head,
+                                out, 1);
+}
+
+static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  const uint32_t* pages, uint32_t page_count, uint32_t physical_pages,
+                                  uint32_t position, uint32_t kv_heads, uint32_t kv_head, uint16_t* out, int order) {
   float scale;
   std::memcpy(&scale, &kScaleBits, 4);
   float m = 0.f, l = 0.f;
@@ -257,12 +390,25 @@ int orc_attention_head(const uint16_t* q, const uint16_t* k_cache, const uint16_
     if (phys >= physical_pages) return 1;
     const uint64_t base = orc_cache_index(phys, slot, kv_heads, kv_head, 0);
     float dot = 0.f;
-    for (int d = 0; d < 128; ++d) {
-      float kf = widen(k_cache[base + d]);
-      float product = qf[d] * kf;
-      float next = dot + product;
-      if (!finite(qf[d]) || !finite(kf) || !finite(product) || !finite(next)) return 1;
-      dot = next;
+    if (order == 0) {
+      for (int d = 0; d < 128; ++d) {
+        float kf = widen(k_cache[base + d]);
+        float product = qf[d] * kf;
+        float next = dot + product;
+        if (!finite(qf[d]) || !finite(kf) || !finite(product) || !finite(next)) return 1;
+        dot = next;
+      }
+    } else {
+      float lanes[64];
+      for (int l = 0; l < 64; ++l) {
+        const float k0 = widen(k_cache[base + l]), k1 = widen(k_cache[base + l + 64]);
+        const float p0 = qf[l] * k0, p1 = qf[l + 64] * k1;
+        const float partial = p0 + p1;
+        if (!finite(p0) || !finite(p1) || !finite(partial)) return 1;
+        lanes[l] = partial;
+      }
+      dot = wave_reduce64(lanes);
+      if (!finite(dot)) return 1;
     }
     float score = dot * scale;
     if (!finite(score)) return 1;
@@ -509,6 +655,12 @@ int orc_threads(void) { return omp_get_max_threads(); }
 struct OrcModel {
   uint32_t layers, hidden, qh, kvh, inter, vocab, tied, theta;
   float eps;
+  // 0: serial (v1) sums; 1: the wave-order profiles; 2: the wave order with
+  // a planted mistake (the gate and up projections narrowed to bf16 by
+  // truncation instead of round-to-nearest-even: a 1-ulp-biased rounding in
+  // one GEMM, which tests use to show that the drift bound between the two
+  // legal orders catches such a bug).
+  int order = 0;
   // row-major bf16 weights, indexed by tensor kind (ferric_hip.h order)
   std::vector<uint16_t> head, embed, final_norm;
   struct Layer {
@@ -543,6 +695,10 @@ OrcModel* orc_model_create(uint32_t layers, uint32_t hidden, uint32_t qh, uint32
 }
 
 void orc_model_destroy(OrcModel* m) { delete m; }
+
+// Reduction order of the model's later steps: 0 serial (v1), 1 wave profiles,
+// 2 wave profiles with the planted gate/up truncation (tests only).
+void orc_model_set_order(OrcModel* m, int order) { m->order = order; }
 
 // Pointer to a weight's row-major storage, resized on first use.
 uint16_t* orc_model_weight(OrcModel* m, uint32_t kind, uint32_t layer, uint64_t elements) {
@@ -623,6 +779,27 @@ void orc_model_kv_fill(OrcModel* m, uint64_t seed, float sigma, const uint32_t* 
 
 // One decoder layer in place on h[rows][hidden], writing K/V to kc/vc.
 // Returns 0, or 1 where the reference would trap.
+// The model's projections and width-H norms in its reduction order (QK-norm
+// keeps the serial width-128 sum in both orders).
+static void model_gemm(OrcModel* m, const uint16_t* a, const uint16_t* b, uint32_t rows, uint32_t n, uint32_t k,
+                       uint16_t* out, float* out_f32, bool planted = false) {
+  if (m->order == 2 && planted && out) {
+    std::vector<float> f((uint64_t)rows * n);
+    orc_gemm_wave(a, b, rows, n, k, nullptr, f.data());
+    for (uint64_t i = 0; i < f.size(); ++i) out[i] = (uint16_t)(bits_of(f[i]) >> 16);  // truncation
+  } else if (m->order >= 1) {
+    orc_gemm_wave(a, b, rows, n, k, out, out_f32);
+  } else {
+    orc_gemm(a, b, nullptr, rows, n, k, 0, out, out_f32);
+  }
+}
+
+static int model_norm(OrcModel* m, const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_t width,
+                      uint16_t* out) {
+  if (m->order >= 1) return orc_rmsnorm_wave(x, w, rows, width, m->eps, out);
+  return orc_rmsnorm(x, nullptr, w, rows, width, m->eps, 0, nullptr, out);
+}
+
 static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const uint32_t* positions,
                      const uint32_t* tables, const uint32_t* page_counts, uint32_t stride, const float* cosr,
                      const float* sinr, uint16_t* kc, uint16_t* vc) {
@@ -632,10 +809,10 @@ static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const 
       kr((uint64_t)rows * KV), attn((uint64_t)rows * Q), gate((uint64_t)rows * I), up((uint64_t)rows * I),
       act((uint64_t)rows * I);
   OrcModel::Layer& W = m->L[l];
-  if (orc_rmsnorm(h, nullptr, W.in_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
-  orc_gemm(xn.data(), W.wq.data(), nullptr, rows, Q, H, 0, q.data(), nullptr);
-  orc_gemm(xn.data(), W.wk.data(), nullptr, rows, KV, H, 0, k.data(), nullptr);
-  orc_gemm(xn.data(), W.wv.data(), nullptr, rows, KV, H, 0, v.data(), nullptr);
+  if (model_norm(m, h, W.in_norm.data(), rows, H, xn.data())) return 1;
+  model_gemm(m, xn.data(), W.wq.data(), rows, Q, H, q.data(), nullptr);
+  model_gemm(m, xn.data(), W.wk.data(), rows, KV, H, k.data(), nullptr);
+  model_gemm(m, xn.data(), W.wv.data(), rows, KV, H, v.data(), nullptr);
   if (orc_rmsnorm(q.data(), nullptr, W.q_norm.data(), rows * QH, 128, m->eps, 0, nullptr, qn.data())) return 1;
   if (orc_rmsnorm(k.data(), nullptr, W.k_norm.data(), rows * KVH, 128, m->eps, 0, nullptr, kn.data())) return 1;
   for (uint32_t r = 0; r < rows; ++r) {
@@ -673,24 +850,24 @@ static int run_layer(OrcModel* m, uint32_t l, uint16_t* h, uint32_t rows, const 
   for (int64_t r = 0; r < (int64_t)rows; ++r)
     for (int64_t hh = 0; hh < (int64_t)QH; ++hh) {
       const uint32_t kvhead = (uint32_t)hh / (QH / KVH);
-      bad |= orc_attention_head(qr.data() + (uint64_t)r * Q + hh * 128, kc, vc, tables + (uint64_t)r * stride,
-                                page_counts[r], m->pages, positions[r], KVH, kvhead,
-                                attn.data() + (uint64_t)r * Q + hh * 128);
+      bad |= attention_head_ordered(qr.data() + (uint64_t)r * Q + hh * 128, kc, vc, tables + (uint64_t)r * stride,
+                                    page_counts[r], m->pages, positions[r], KVH, kvhead,
+                                    attn.data() + (uint64_t)r * Q + hh * 128, m->order >= 1 ? 1 : 0);
     }
   if (bad) return 1;
   // O projection: FP32 partial, then the TP1 residual.
   {
     std::vector<float> part((uint64_t)rows * H);
-    orc_gemm(attn.data(), W.wo.data(), nullptr, rows, H, Q, 0, nullptr, part.data());
+    model_gemm(m, attn.data(), W.wo.data(), rows, H, Q, nullptr, part.data());
     if (orc_residual(part.data(), h, (uint64_t)rows * H, h, nullptr)) return 1;
   }
-  if (orc_rmsnorm(h, nullptr, W.post_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
-  orc_gemm(xn.data(), W.wg.data(), nullptr, rows, I, H, 0, gate.data(), nullptr);
-  orc_gemm(xn.data(), W.wu.data(), nullptr, rows, I, H, 0, up.data(), nullptr);
+  if (model_norm(m, h, W.post_norm.data(), rows, H, xn.data())) return 1;
+  model_gemm(m, xn.data(), W.wg.data(), rows, I, H, gate.data(), nullptr, true);
+  model_gemm(m, xn.data(), W.wu.data(), rows, I, H, up.data(), nullptr, true);
   if (orc_swiglu(gate.data(), up.data(), (uint64_t)rows * I, act.data())) return 1;
   {
     std::vector<float> part((uint64_t)rows * H);
-    orc_gemm(act.data(), W.wd.data(), nullptr, rows, H, I, 0, nullptr, part.data());
+    model_gemm(m, act.data(), W.wd.data(), rows, H, I, nullptr, part.data());
     if (orc_residual(part.data(), h, (uint64_t)rows * H, h, nullptr)) return 1;
   }
   return 0;
@@ -722,9 +899,9 @@ int orc_model_forward(OrcModel* m, const uint32_t* tokens, const uint32_t* posit
   }
   t_layers_end = omp_get_wtime();
   const int fail = 1 + (int)m->layers;
-  if (orc_rmsnorm(h.data(), nullptr, m->final_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return fail;
+  if (model_norm(m, h.data(), m->final_norm.data(), rows, H, xn.data())) return fail;
   std::vector<float> lg((uint64_t)rows * V);
-  orc_gemm(xn.data(), m->tied ? m->embed.data() : m->head.data(), nullptr, rows, V, H, 0, nullptr, lg.data());
+  model_gemm(m, xn.data(), m->tied ? m->embed.data() : m->head.data(), rows, V, H, nullptr, lg.data());
   for (uint32_t r = 0; r < rows; ++r) {
     float gap = 0.f;
     uint32_t c = orc_argmax_f32(lg.data() + (uint64_t)r * V, V, &gap);
@@ -749,8 +926,8 @@ int orc_model_head(OrcModel* m, const uint16_t* hidden_in, uint32_t rows, float*
                    float* gaps) {
   const uint32_t H = m->hidden, V = m->vocab;
   std::vector<uint16_t> xn((uint64_t)rows * H);
-  if (orc_rmsnorm(hidden_in, nullptr, m->final_norm.data(), rows, H, m->eps, 0, nullptr, xn.data())) return 1;
-  orc_gemm(xn.data(), m->tied ? m->embed.data() : m->head.data(), nullptr, rows, V, H, 0, nullptr, logits);
+  if (model_norm(m, hidden_in, m->final_norm.data(), rows, H, xn.data())) return 1;
+  model_gemm(m, xn.data(), m->tied ? m->embed.data() : m->head.data(), rows, V, H, nullptr, logits);
   for (uint32_t r = 0; r < rows; ++r) {
     float gap = 0.f;
     const uint32_t c = orc_argmax_f32(logits + (uint64_t)r * V, V, &gap);
@@ -765,13 +942,18 @@ int orc_model_head(OrcModel* m, const uint16_t* hidden_in, uint32_t rows, float*
 // [rows][hidden] to hidden_out, against a scratch copy of that layer's KV
 // (the model's pool is left untouched). Used to measure one layer's numerical
 // error on the GPU's own input. Returns 0, or 1 where the reference traps.
+// kc_in / vc_in (may be NULL): the layer's K and V pools to start from
+// instead of the model's own (e.g. another implementation's KV history, so
+// that only the layer's own arithmetic differs).
 int orc_model_layer_isolated(OrcModel* m, uint32_t layer, const uint16_t* hidden_in, const uint32_t* positions,
                              const uint32_t* tables, const uint32_t* page_counts, uint32_t stride, uint32_t rows,
-                             uint16_t* hidden_out) {
+                             const uint16_t* kc_in, const uint16_t* vc_in, uint16_t* hidden_out) {
   const uint64_t n = (uint64_t)rows * m->hidden;
   std::memcpy(hidden_out, hidden_in, n * 2);
-  std::vector<uint16_t> kc(m->cache(layer, 0), m->cache(layer, 0) + m->slab());
-  std::vector<uint16_t> vc(m->cache(layer, 1), m->cache(layer, 1) + m->slab());
+  const uint16_t* k0 = kc_in ? kc_in : m->cache(layer, 0);
+  const uint16_t* v0 = vc_in ? vc_in : m->cache(layer, 1);
+  std::vector<uint16_t> kc(k0, k0 + m->slab());
+  std::vector<uint16_t> vc(v0, v0 + m->slab());
   std::vector<float> cosr((uint64_t)rows * 64), sinr((uint64_t)rows * 64);
   for (uint32_t r = 0; r < rows; ++r) orc_rope_table(positions[r], m->theta, &cosr[r * 64ull], &sinr[r * 64ull]);
   return run_layer(m, layer, hidden_out, rows, positions, tables, page_counts, stride, cosr.data(), sinr.data(),

@@ -88,6 +88,17 @@ def lib():
         L.orc_synth_scale.restype = ctypes.c_float
         L.orc_threads.argtypes = []
         L.orc_threads.restype = ctypes.c_int
+        L.orc_gemm_wave.argtypes = [_u16p, _u16p, _c_u32, _c_u32, _c_u32, _u16p, _f32p]
+        L.orc_gemm_wave.restype = None
+        L.orc_square_sum_wave.argtypes = [_u16p, _c_u32]
+        L.orc_square_sum_wave.restype = ctypes.c_float
+        L.orc_rmsnorm_wave.argtypes = [_u16p, _u16p, _c_u32, _c_u32, ctypes.c_float, _u16p]
+        L.orc_rmsnorm_wave.restype = ctypes.c_int
+        L.orc_attention_head_wave.argtypes = [_u16p, _u16p, _u16p, _u32p, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32,
+                                              _u16p]
+        L.orc_attention_head_wave.restype = ctypes.c_int
+        L.orc_model_set_order.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.orc_model_set_order.restype = None
         L.orc_model_create.argtypes = [_c_u32] * 8 + [ctypes.c_float, _c_u32]
         L.orc_model_create.restype = ctypes.c_void_p
         L.orc_model_destroy.argtypes = [ctypes.c_void_p]
@@ -102,7 +113,7 @@ def lib():
                                         _u16p, _f32p, ctypes.POINTER(ctypes.c_double)]
         L.orc_model_forward.restype = ctypes.c_int
         L.orc_model_layer_isolated.argtypes = [ctypes.c_void_p, _c_u32, _u16p, _u32p, _u32p, _u32p, _c_u32, _c_u32,
-                                               _u16p]
+                                               _u16p, _u16p, _u16p]
         L.orc_model_layer_isolated.restype = ctypes.c_int
         L.orc_model_head.argtypes = [ctypes.c_void_p, _u16p, _c_u32, _f32p, _u32p, _f32p]
         L.orc_model_head.restype = ctypes.c_int
@@ -134,6 +145,43 @@ def bf16_from_f32_scalar(v: float) -> int:
 def square_sum(x):
     x = np.ascontiguousarray(x, dtype=np.uint16)
     return float(np.float32(lib().orc_square_sum(_ptr(x, _u16p), len(x))))
+
+
+def square_sum_wave(x):
+    """Sum of squares in the wave profile's order (lane l: x[l + 64 c]^2, then
+    the 64-lane butterfly)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    return float(np.float32(lib().orc_square_sum_wave(_ptr(x, _u16p), len(x))))
+
+
+def rmsnorm_wave(x, weight, rows, width, eps=1e-6):
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    weight = np.ascontiguousarray(weight, dtype=np.uint16)
+    out = np.zeros(rows * width, dtype=np.uint16)
+    st = lib().orc_rmsnorm_wave(_ptr(x, _u16p), _ptr(weight, _u16p), rows, width, eps, _ptr(out, _u16p))
+    return None if st else out
+
+
+def gemm_wave(a, b, m, n, k, f32_out=False):
+    """A W^T in the wave-GEMV order (k % 64 == 0)."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    if f32_out:
+        out = np.zeros(m * n, np.float32)
+        lib().orc_gemm_wave(_ptr(a, _u16p), _ptr(b, _u16p), m, n, k, None, _ptr(out, _f32p))
+    else:
+        out = np.zeros(m * n, np.uint16)
+        lib().orc_gemm_wave(_ptr(a, _u16p), _ptr(b, _u16p), m, n, k, _ptr(out, _u16p), None)
+    return out
+
+
+def attention_head_wave(q, kc, vc, pages, physical_pages, position, kv_heads, kv_head):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    pages = np.ascontiguousarray(pages, dtype=np.uint32)
+    out = np.zeros(128, np.uint16)
+    st = lib().orc_attention_head_wave(_ptr(q, _u16p), _ptr(kc, _u16p), _ptr(vc, _u16p), _ptr(pages, _u32p),
+                                       len(pages), physical_pages, position, kv_heads, kv_head, _ptr(out, _u16p))
+    return None if st else out
 
 
 def square_sum_bits(x) -> int:
@@ -329,8 +377,28 @@ class Model:
         lib().orc_model_kv_fill(self.h, seed, sigma, _ptr(tables, _u32p), stride, _ptr(lengths, _u32p),
                                 _ptr(keys, _u64p), len(lengths), context_stride)
 
-    def layer_isolated(self, layer, hidden_in, positions, tables, page_counts, stride):
-        """One layer from a given input residual stream (scratch KV copy)."""
+    def set_order(self, order: int):
+        """Reduction order of later calls: 0 = the reference's serial (v1)
+        sums, 1 = its wave-order profiles (v5 GEMV, v15 RMSNorm, v14 attention),
+        2 = order 1 with a planted mistake (gate/up narrowed by truncation), for
+        tests that show a drift bound catches a 1-ulp-biased rounding."""
+        lib().orc_model_set_order(self.h, int(order))
+
+    def layer_isolated(self, layer, hidden_in, positions, tables, page_counts, stride, order=None, kv=None):
+        """One layer from a given input residual stream (on a scratch copy of
+        the layer's KV pool, or of kv = (K pool, V pool) when given); order:
+        reduction order for this call only."""
+        if order is not None:
+            self.set_order(order)
+            try:
+                return self.layer_isolated(layer, hidden_in, positions, tables, page_counts, stride, kv=kv)
+            finally:
+                self.set_order(0)
+        kin = vin = None
+        if kv is not None:
+            n = self.pages * 16 * self.desc["kv_heads"] * 128
+            kin, vin = (np.ascontiguousarray(a, np.uint16) for a in kv)
+            assert kin.size == n and vin.size == n
         hidden_in = np.ascontiguousarray(hidden_in, np.uint16).reshape(-1)
         positions = np.ascontiguousarray(positions, np.uint32)
         tables = np.ascontiguousarray(tables, np.uint32)
@@ -338,13 +406,19 @@ class Model:
         out = np.zeros_like(hidden_in)
         st = lib().orc_model_layer_isolated(self.h, layer, _ptr(hidden_in, _u16p), _ptr(positions, _u32p),
                                             _ptr(tables, _u32p), _ptr(page_counts, _u32p), stride, len(positions),
-                                            _ptr(out, _u16p))
+                                            _ptr(kin, _u16p), _ptr(vin, _u16p), _ptr(out, _u16p))
         if st:
             raise RuntimeError("oracle layer trapped")
         return out.reshape(len(positions), -1)
 
-    def head(self, hidden_in):
+    def head(self, hidden_in, order=None):
         """Final RMSNorm + FP32 head + argmax on a given residual stream."""
+        if order is not None:
+            self.set_order(order)
+            try:
+                return self.head(hidden_in)
+            finally:
+                self.set_order(0)
         hidden_in = np.ascontiguousarray(hidden_in, np.uint16)
         rows = hidden_in.size // self.desc["hidden"]
         logits = np.zeros(rows * self.desc["vocabulary"], np.float32)
@@ -356,7 +430,16 @@ class Model:
             raise RuntimeError("oracle head trapped")
         return {"logits": logits.reshape(rows, -1), "choices": choices, "gaps": gaps}
 
-    def forward(self, tokens, positions, tables, page_counts, stride, want_logits=True, want_hidden=False):
+    def forward(self, tokens, positions, tables, page_counts, stride, want_logits=True, want_hidden=False,
+                order=None):
+        """One step (KV rows appended in place). order: reduction order for this
+        call only (default: the model's current one)."""
+        if order is not None:
+            self.set_order(order)
+            try:
+                return self.forward(tokens, positions, tables, page_counts, stride, want_logits, want_hidden)
+            finally:
+                self.set_order(0)
         d = self.desc
         rows = len(tokens)
         tokens = np.ascontiguousarray(tokens, np.uint32)

@@ -385,3 +385,93 @@ def test_synth_generator_pins():
     assert abs(vals.std() - 0.02) < 4e-4
     assert np.max(np.abs(vals)) <= 0.02 * 3.47
     assert orc.synth_scale(1.0) == np.float32(1.0 / 37837.2306413553)
+
+
+# ---- the wave-order profiles (a second legal reduction order) ----------------
+# device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15-137 (GEMV lanes
+# k = 64 s + l), device/qwen3-tp-wave-rmsnorm-kernels-v15/src/rmsnorm.rs:60-75
+# (lane l: x[l + 64 c]^2), device/qwen3-tp-wave-query-hoist-kernels-v14/src/
+# attention.rs:174-217 (lane l: q[l] k[l] + q[l+64] k[l+64]); the 64-lane
+# reduction is the xor butterfly (fe2o3's own tree is not in the reference).
+# Cancellation at 2^24 (where +1 is absorbed) makes each order visible.
+
+def test_wave_gemm_known_answers():
+    k = 128
+    a = np.full(k, 0x3F80, np.uint16)  # ones
+    w = np.zeros(k, np.uint16)
+    w[0], w[64], w[1] = 0x4B80, 0xCB80, 0x3F80  # 2^24 and -2^24 in lane 0 (steps 0, 1), 1 in lane 1
+    assert orc.gemm(a, w, 1, 1, k, f32_out=True)[0] == 0.0  # serial: 2^24 + 1 absorbs the 1
+    assert orc.gemm_wave(a, w, 1, 1, k, f32_out=True)[0] == 1.0  # lane 0 cancels before lane 1 joins
+    w = np.zeros(k, np.uint16)
+    w[0], w[32], w[1] = 0x4B80, 0xCB80, 0x3F80  # lanes 0 and 32 meet first in the butterfly
+    assert orc.gemm_wave(a, w, 1, 1, k, f32_out=True)[0] == 1.0
+    w = np.zeros(k, np.uint16)
+    w[0], w[1], w[2] = 0x4B80, 0xCB80, 0x3F80  # lanes 0 and 1 meet last: 2^24 + 1 absorbs first
+    assert orc.gemm_wave(a, w, 1, 1, k, f32_out=True)[0] == 0.0
+    # exact sums agree with the serial order bit for bit: the 2x3x4 KAT
+    # (gemm reference.rs:137-153) zero-padded to k = 64
+    A = np.zeros((2, 64), np.uint16)
+    B = np.zeros((3, 64), np.uint16)
+    A[:, :4] = [[0x3F80, 0x4000, 0x4040, 0x4080], [0xBF80, 0x3F00, 0x4000, 0xC000]]
+    B[:, :4] = [[0x3F80, 0x0000, 0x3F80, 0x0000], [0x0000, 0x3F80, 0x0000, 0x3F80], [0x3F00, 0x3F00, 0x3F00, 0x3F00]]
+    got = orc.gemm_wave(A.reshape(-1), B.reshape(-1), 2, 3, 64)
+    assert got.tolist() == orc.gemm(A.reshape(-1), B.reshape(-1), 2, 3, 64).tolist()
+
+
+def test_wave_square_sum_known_answer():
+    # 4096^2 = 2^24 in lane 0 plus 127 ones: the serial sum absorbs every one
+    # (2^24 + 1 rounds to even); in wave order lanes 1..63 first build 2, 4, ...
+    # so the butterfly adds 2 + 4 + 8 + 16 + 32 + 64 = 126 exactly.
+    x = np.full(128, 0x3F80, np.uint16)
+    x[0] = 0x4580
+    assert orc.square_sum(x) == 2.0 ** 24
+    assert orc.square_sum_wave(x) == 2.0 ** 24 + 126
+    # the normalize-and-weight step is the serial one: equal bits on a row
+    # whose sum is exact in either order
+    r = np.random.default_rng(3).integers(-8, 9, 1024).astype(np.float32)
+    xb = orc.f32_to_bf16(r)
+    w = np.full(1024, 0x3F80, np.uint16)
+    assert np.array_equal(orc.rmsnorm_wave(xb, w, 1, 1024), orc.rmsnorm(xb, w, 1, 1024))
+
+
+def test_wave_attention_score_known_answer():
+    # Two keys; key 0's dot is 2^24 + 1 - 2^24 with the terms in dims 0, 1, 64:
+    # serial order absorbs the 1 (score 0, the zero-score mean 0x3f00 of
+    # paged-decode reference.rs:200-225), wave order cancels dims 0 and 64 in
+    # lane 0 first (dot 1, score = f32(0x3db504f3)). V: key 0 ones, key 1 zeros,
+    # so the output is 1 / (1 + e^-scale) = 0.5221 -> bf16 0x3f06.
+    kvh, pages = 1, 1
+    kc = np.zeros(pages * 16 * kvh * 128, np.uint16)
+    vc = np.zeros_like(kc)
+    q = np.zeros(128, np.uint16)
+    q[0], q[1], q[64] = 0x4B80, 0x3F80, 0x4B80
+    kc[0], kc[1], kc[64] = 0x3F80, 0x3F80, 0xBF80
+    vc[:128] = 0x3F80
+    table = np.array([0], np.uint32)
+    serial = orc.attention_head(q, kc, vc, table, pages, 1, kvh, 0)
+    wave = orc.attention_head_wave(q, kc, vc, table, pages, 1, kvh, 0)
+    assert np.all(serial == 0x3F00)
+    scale = float(np.array([0x3DB504F3], np.uint32).view(np.float32)[0])
+    want = int(orc.f32_to_bf16(np.float32(1.0 / (1.0 + math.exp(-scale)))))
+    assert want == 0x3F06 and np.all(wave == want)
+
+
+def test_model_orders_differ_only_by_reassociation():
+    # Two legal orders on a small model: every layer within the per-layer bar
+    # of the other, greedy ids equal except at near-ties.
+    cfg = dict(layers=2, hidden=256, query_heads=4, kv_heads=2, head_dim=128, intermediate=512, vocabulary=512,
+               tied_embedding=1, rope_theta=1_000_000, rms_epsilon=1e-6)
+    m = orc.Model(cfg, 16)
+    try:
+        m.synthesize(5, 0.02)
+        toks, pos = [3, 7, 11], [0, 1, 2]
+        tables = np.zeros((3, 2), np.uint32)
+        counts = np.ones(3, np.uint32)
+        a = m.forward(toks, pos, tables, counts, 2, want_hidden=True, order=1)
+        b = m.forward(toks, pos, tables, counts, 2, want_hidden=True)
+        assert not np.array_equal(a["logits"], b["logits"])  # the orders do differ
+        assert float(np.max(np.abs(a["logits"] - b["logits"]))) < 1e-2
+        for i, (ca, cb) in enumerate(zip(a["choices"], b["choices"])):
+            assert ca == cb or b["gaps"][i] < 1e-2
+    finally:
+        m.close()
