@@ -366,7 +366,8 @@ int orc_attention_head(const uint16_t* q, const uint16_t* k_cache, const uint16_
                                 out, 0);
 }
 
-// The same head with the score dot in wave order (v14 attention.rs:174-217).
+// The same head in the split-context wave-order profile (v21 partitions with
+// v14 score dots), below.
 int orc_attention_head_wave(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                             const uint32_t* pages, uint32_t page_count, uint32_t physical_pages, uint32_t position,
                             uint32_t kv_heads, uint32_t kv_head, uint16_t* out) {
@@ -374,16 +375,17 @@ int orc_attention_head_wave(const uint16_t* q, const uint16_t* k_cache, const ui
                                 out, 1);
 }
 
-static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                  const uint32_t* pages, uint32_t page_count, uint32_t physical_pages,
-                                  uint32_t position, uint32_t kv_heads, uint32_t kv_head, uint16_t* out, int order) {
+// Online-softmax state of the keys [begin, end) of one head: t = begin gives
+// m = s, l = 1, n = v; later keys m' = max(m, s), l = l e^(m-m') + e^(s-m'),
+// n likewise (paged_decode.rs:222-572). order 0: serial 128-wide score dot;
+// order 1: the wave-order dot. Returns 1 where the reference traps.
+static int attention_span(const float* qf, const uint16_t* k_cache, const uint16_t* v_cache, const uint32_t* pages,
+                          uint32_t page_count, uint32_t physical_pages, uint32_t begin, uint32_t end,
+                          uint32_t kv_heads, uint32_t kv_head, int order, float* m_out, float* l_out, float* n) {
   float scale;
   std::memcpy(&scale, &kScaleBits, 4);
   float m = 0.f, l = 0.f;
-  float n[128] = {};
-  float qf[128];
-  for (int d = 0; d < 128; ++d) qf[d] = widen(q[d]);
-  for (uint32_t t = 0; t <= position; ++t) {
+  for (uint32_t t = begin; t < end; ++t) {
     uint32_t lp = t / 16, slot = t % 16;
     if (lp >= page_count) return 1;
     uint32_t phys = pages[lp];
@@ -400,19 +402,19 @@ static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, co
       }
     } else {
       float lanes[64];
-      for (int l = 0; l < 64; ++l) {
-        const float k0 = widen(k_cache[base + l]), k1 = widen(k_cache[base + l + 64]);
-        const float p0 = qf[l] * k0, p1 = qf[l + 64] * k1;
+      for (int ln = 0; ln < 64; ++ln) {
+        const float k0 = widen(k_cache[base + ln]), k1 = widen(k_cache[base + ln + 64]);
+        const float p0 = qf[ln] * k0, p1 = qf[ln + 64] * k1;
         const float partial = p0 + p1;
         if (!finite(p0) || !finite(p1) || !finite(partial)) return 1;
-        lanes[l] = partial;
+        lanes[ln] = partial;
       }
       dot = wave_reduce64(lanes);
       if (!finite(dot)) return 1;
     }
     float score = dot * scale;
     if (!finite(score)) return 1;
-    if (t == 0) {
+    if (t == begin) {
       m = score;
       l = 1.f;
       for (int d = 0; d < 128; ++d) {
@@ -435,8 +437,57 @@ static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, co
       l = next_l;
     }
   }
+  *m_out = m;
+  *l_out = l;
+  return 0;
+}
+
+// order 0: qwen3_paged_gqa_decode_bf16_f32_v1, one serial recurrence over keys
+// 0..=position. order 1: the reference's split-context profile
+// (device/qwen3-tp-c1-split8-attention-kernels-v21/src/attention.rs:16-213,
+// merge :214-308): 8 contiguous partitions of ceil(keys / 8) keys, each its
+// own recurrence with wave-order score dots (v14), then the partition states
+// merged in ascending order by the same recurrence (a partition's m and l in
+// place of a key's score and 1), divided and narrowed once.
+static int attention_head_ordered(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  const uint32_t* pages, uint32_t page_count, uint32_t physical_pages,
+                                  uint32_t position, uint32_t kv_heads, uint32_t kv_head, uint16_t* out, int order) {
+  float qf[128];
+  for (int d = 0; d < 128; ++d) qf[d] = widen(q[d]);
+  const uint32_t keys = position + 1;
+  float M = 0.f, L = 0.f, N[128];
+  if (order == 0) {
+    if (attention_span(qf, k_cache, v_cache, pages, page_count, physical_pages, 0, keys, kv_heads, kv_head, 0, &M, &L,
+                       N))
+      return 1;
+  } else {
+    const uint32_t span = (keys + 7) / 8;
+    for (uint32_t p = 0; p < 8 && p * span < keys; ++p) {
+      float m, l, n[128];
+      const uint32_t begin = p * span, end = std::min(keys, begin + span);
+      if (attention_span(qf, k_cache, v_cache, pages, page_count, physical_pages, begin, end, kv_heads, kv_head, 1,
+                         &m, &l, n))
+        return 1;
+      if (p == 0) {
+        M = m;
+        L = l;
+        std::memcpy(N, n, sizeof(N));
+      } else {
+        const float next_max = m > M ? m : M;
+        const float pw = std::exp(M - next_max);
+        const float cw = std::exp(m - next_max);
+        L = L * pw + l * cw;
+        if (!finite(pw) || !finite(cw) || !finite(L) || L <= 0.f) return 1;
+        for (int d = 0; d < 128; ++d) {
+          N[d] = N[d] * pw + n[d] * cw;
+          if (!finite(N[d])) return 1;
+        }
+        M = next_max;
+      }
+    }
+  }
   for (int d = 0; d < 128; ++d) {
-    float o = n[d] / l;
+    float o = N[d] / L;
     uint16_t b = narrow(o);
     if (!finite(o) || !finite_bf16(b)) return 1;
     out[d] = b;

@@ -25,9 +25,9 @@ from __future__ import annotations
 import numpy as np
 
 # A layer's own error (the run's layer output against the serial oracle's
-# layer on the same input) is measured as a relative RMS over the whole
-# residual stream, and its mean over the layers may be at most LAYER_FACTOR
-# times the wave-order oracle's on the same inputs. The maximum element error
+# layer on the same input and KV history) is measured as a relative RMS over
+# the whole residual stream, and its mean over the layer outputs a test checks
+# may be at most LAYER_FACTOR times the wave-order oracle's on the same inputs. The maximum element error
 # does not separate a legal reassociation from a bug (both saturate at a bf16
 # ulp or two of the row maximum); the RMS counts how many elements move.
 # Measured on the CPU (Qwen3-0.6B shape, 28 layers, batch 32): wave-vs-serial

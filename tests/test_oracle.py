@@ -475,3 +475,36 @@ def test_model_orders_differ_only_by_reassociation():
             assert ca == cb or b["gaps"][i] < 1e-2
     finally:
         m.close()
+
+
+def test_split_context_attention_is_the_softmax():
+    # The wave-order attention splits the keys into 8 partitions (v21) and
+    # merges their states; both orders must be the softmax-weighted mean of V
+    # (float64 closed form) to within a bf16 ulp of the output, for contexts
+    # that leave empty, single-key and uneven partitions.
+    r = np.random.default_rng(17)
+    kvh, pages = 2, 8
+    kc = orc.f32_to_bf16(r.standard_normal(pages * 16 * kvh * 128).astype(np.float32))
+    vc = orc.f32_to_bf16(r.standard_normal(pages * 16 * kvh * 128).astype(np.float32))
+    table = r.permutation(pages).astype(np.uint32)
+    scale = float(np.array([0x3DB504F3], np.uint32).view(np.float32)[0])
+    differ = 0
+    for position in (0, 1, 6, 7, 8, 9, 30, 63, 64, 100, 127):
+        for head in range(kvh):
+            q = orc.f32_to_bf16((r.standard_normal(128) * 2).astype(np.float32))
+            qf = orc.bf16_to_f32(q).astype(np.float64)
+            k_rows, v_rows = [], []
+            for t in range(position + 1):
+                base = orc.cache_index(int(table[t // 16]), t % 16, kvh, head, 0)
+                k_rows.append(orc.bf16_to_f32(kc[base:base + 128]).astype(np.float64))
+                v_rows.append(orc.bf16_to_f32(vc[base:base + 128]).astype(np.float64))
+            s = np.array([qf @ k for k in k_rows]) * scale
+            w = np.exp(s - s.max())
+            exact = (w[:, None] * np.array(v_rows)).sum(0) / w.sum()
+            ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+            serial = orc.attention_head(q, kc, vc, table, pages, position, kvh, head)
+            split = orc.attention_head_wave(q, kc, vc, table, pages, position, kvh, head)
+            for got in (serial, split):
+                assert np.all(np.abs(orc.bf16_to_f32(got) - exact) <= ulp + 1e-6), (position, head)
+            differ += int(not np.array_equal(serial, split))
+    assert differ > 0  # the two orders are distinct arithmetic
