@@ -3,6 +3,7 @@
 // shapes on the host before launching, so a kernel never sees a geometry it
 // was not written for.
 #include <cstring>
+#include <mutex>
 
 #include "../../include/ferric_hip.h"
 #include "kernels.hpp"
@@ -122,6 +123,88 @@ fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint1
   return from_hip(fh::launch_qknorm_rope_kv(bf, part, qkv_splits, q_norm, k_norm, cos_table, sin_table, positions,
                                             page_table, q_out, k_cache, v_cache, rows, query_heads, kv_heads, stride,
                                             physical_pages, context_tokens, epsilon, error_word, as_stream(stream)));
+}
+
+}  // extern "C"
+
+// ---- no-allocation attention ----------------------------------------------
+// fh_op_paged_attention_noalloc keeps its partition records in this
+// file-scope device array instead of a caller workspace. In host code
+// `scratch` is only a stand-in symbol: its device address is resolved once
+// per device (hipGetSymbolAddress, with that device current) and only that
+// address is ever handed to kernels. Every call on a GPU shares the GPU's
+// copy, so calls that overlap on one GPU race; each call writes every record
+// it later reads, so nothing needs clearing between calls.
+namespace {
+constexpr uint64_t kNoAllocAttnRecords = 16384;  // rows x query heads x 512-token partitions (8.5 MB)
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kNoAllocMaxDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocAttnRecords * fh::kAttnPartialFloats];
+
+namespace {
+// The device address of `scratch` on the stream's device (NULL and an error
+// message on failure).
+float* noalloc_scratch(hipStream_t s) {
+  int dev = -1;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) {
+    fh::set_thread_error(e != hipSuccess ? hipGetErrorString(e) : "device ordinal out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess || !ptr) {
+      fh::set_thread_error(e != hipSuccess ? hipGetErrorString(e) : "no device address for the scratch array");
+      return nullptr;
+    }
+    g_scratch_dev[dev] = ptr;
+  }
+  return reinterpret_cast<float*>(g_scratch_dev[dev]);
+}
+}  // namespace
+
+extern "C" {
+
+fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                        const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
+                                        uint32_t out_tiled, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                                        uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
+                                        uint32_t* error_word, void* stream) {
+  if (!q || !k_cache || !v_cache || !positions || !page_table || !out || rows == 0 || kv_heads == 0 ||
+      query_heads % kv_heads != 0 || stride == 0 || physical_pages == 0 || context_tokens == 0 ||
+      (uint64_t)stride * 16 < context_tokens)
+    return FH_ERR_INVALID_ARGUMENT;
+  const uint32_t g = query_heads / kv_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
+  const uint64_t records = (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens);
+  if (records > kNoAllocAttnRecords) {
+    fh::set_thread_error("fh_op_paged_attention_noalloc: rows x query_heads x ceil(context_tokens / 512) exceeds the "
+                         "16384 partition records of its static scratch");
+    return FH_ERR_INVALID_ARGUMENT;
+  }
+  hipStream_t s = as_stream(stream);
+  float* part = noalloc_scratch(s);
+  if (!part) return FH_ERR_DEVICE;
+  (void)hipGetLastError();
+  hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,
+                                              rows, rows, query_heads, kv_heads, stride, physical_pages,
+                                              context_tokens, error_word, s);
+  if (e == hipSuccess)
+    e = fh::launch_attention_merge(part, positions, out, out_tiled, 0, rows, rows, query_heads, context_tokens,
+                                   error_word, s);
+  return status_of(e);
 }
 
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens) {

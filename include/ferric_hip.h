@@ -282,6 +282,20 @@ fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, cons
                                 uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
                                 uint32_t* error_word, void* stream);
 
+/* No counterpart in the reference: fh_op_paged_attention without a workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The partition records live in a
+ * static device array of the library, 16384 records (rows x query_heads x
+ * ceil(context_tokens / 512)) = 8.5 MB, held on every GPU the entry point has run
+ * on until the process ends; larger launches return FH_ERR_INVALID_ARGUMENT.
+ * Calls that overlap on one GPU share that array and race. Same kernels and results
+ * as fh_op_paged_attention. */
+fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                        const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
+                                        uint32_t out_tiled, uint32_t rows, uint32_t query_heads, uint32_t kv_heads,
+                                        uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
+                                        uint32_t* error_word, void* stream);
+
 /* K6 SwiGLU as its own kernel: out = bf16(silu(g) * u), the stable-sigmoid form of
  * qwen3_swiglu_bf16_f32_v1 (device/qwen3-all-kernels-v1/src/swiglu.rs:62-120). */
 fh_status fh_op_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, uint64_t elements,
