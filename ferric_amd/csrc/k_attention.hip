@@ -7,15 +7,15 @@
 // reference's split variant (device/qwen3-tp-c1-split8-attention-kernels-v21,
 // README.md:42-80) partitions the context, keeps an FP32 state (m, l, n[128])
 // per partition, merges the partitions in ascending order, then divides and
-// narrows once. This kernel pair keeps that contract with kAttnSplitPages-page
-// partitions.
+// narrows once. These kernels keep that contract with 16- or 32-page
+// partitions (attn_split_pages).
 //
 // K and V are read once per step, so their loads are non-temporal: letting
 // them allocate in the caches cost about 13% of the kernel's time (measured
 // with 32 rows of mean context 4K, 550 MB of K/V per layer).
 //
 // Partition kernel, grid (partition, KV head, row), 8 waves; each wave takes
-// 4 of the partition's 32 pages and the G query heads of the KV head, so
+// PP / 8 of the partition's PP pages and the G query heads of the KV head, so
 // every K/V byte is read once per token row. A wave makes two memory round
 // trips, each with all of its pages' loads in flight at once:
 //   1. K: whole 256-byte token rows per load, re-laid through a padded LDS
@@ -28,10 +28,13 @@
 //      is one coalesced 256-byte wave load.
 // The eight wave states (m, l, n[128]) are merged in wave order. A row whose
 // context fits one partition is finished here (divide, narrow, store);
-// longer rows leave partition states for the merge kernel.
-// Merge kernel: one wave per (row, query head). Partition weights
+// longer rows leave partition states, merged either by the merge kernel or,
+// in the fused form, by the partition workgroup of each (row, KV head) that
+// finishes last (a per-pair arrival counter; it resets the counter).
+// Merge (merge_records, in either kernel): partition weights
 // w_p = exp(m_p - M) with M the maximum over partitions, then l and n are
-// summed over partitions in ascending order, divided, narrowed once.
+// summed over partitions in ascending order, divided, narrowed once. Both
+// forms run the same code on the same records, so their outputs are equal.
 #include <type_traits>
 
 #include "common.hpp"
@@ -67,22 +70,79 @@ __device__ __forceinline__ void store_head(uint16_t* out, uint32_t out_mtiles, u
     reinterpret_cast<uint32_t*>(out + ((uint64_t)(row0 + r) * qh + head) * 128)[lane] = word;
 }
 
+// Merges the ns partition records at p (one (row, query head), records of
+// kAttnPartialFloats floats) in ascending partition order; this lane's
+// output dims 2 lane, 2 lane + 1 come back unnormalised in n0, n1 with the
+// denominator L.
+template <bool COHERENT = false>
+__device__ __forceinline__ float load_record(const float* p) {
+  if constexpr (COHERENT)
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+
+// COHERENT: every record load is an agent-scope atomic load (records written
+// in the same launch by workgroups on other XCDs, see the partition kernel).
+template <bool COHERENT = false>
+__device__ __forceinline__ void merge_records(const float* p, uint32_t ns, int lane, float& L, float& n0,
+                                              float& n1) {
+  const float kNegInf = -__builtin_inff();
+  float mloc = kNegInf;
+  for (uint32_t sp = lane; sp < ns; sp += 64) mloc = fmaxf(mloc, load_record<COHERENT>(p + (uint64_t)sp * kAttnPartialFloats));
+  const float M = wave_max(mloc);
+  L = 0.f;
+  n0 = 0.f;
+  n1 = 0.f;
+  for (uint32_t c0 = 0; c0 < ns; c0 += 64) {
+    // Lane s holds partition c0 + s's weight exp(m - M) and weighted l.
+    const uint32_t mine = c0 + lane;
+    const float ms = mine < ns ? load_record<COHERENT>(p + (uint64_t)mine * kAttnPartialFloats) : kNegInf;
+    const float ws = mine < ns ? expf(ms - M) : 0.f;
+    const float lw = mine < ns ? load_record<COHERENT>(p + (uint64_t)mine * kAttnPartialFloats + 1) * ws : 0.f;
+    const uint32_t cn = min(64u, ns - c0);
+    for (uint32_t s0 = 0; s0 < cn; s0 += 8) {
+      // Eight partitions' numerators in flight, then added in ascending order.
+      float a0[8], a1[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t sp = s0 + u;
+        const float* ps = p + (uint64_t)(c0 + sp) * kAttnPartialFloats;
+        a0[u] = sp < cn ? load_record<COHERENT>(ps + 2 + 2 * lane) : 0.f;
+        a1[u] = sp < cn ? load_record<COHERENT>(ps + 3 + 2 * lane) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t sp = s0 + u;
+        if (sp < cn) {
+          const float w = lane_bcast(ws, (int)sp);
+          L += lane_bcast(lw, (int)sp);
+          n0 += a0[u] * w;
+          n1 += a1[u] * w;
+        }
+      }
+    }
+  }
+}
+
 // One workgroup per (partition, KV head, row); its WAVES waves split the
-// partition's pages (kAttnSplitPages / WAVES each) and serve the G query
-// heads of the KV head. A wave issues all of its K loads at once, scores them,
-// then issues all of its V loads at once: two memory round trips per wave.
-template <int G, int WAVES>
+// partition's PP pages (PP / WAVES each) and serve the G query heads of the
+// KV head. A wave issues all of its K loads at once, scores them, then
+// issues all of its V loads at once: two memory round trips per wave.
+// FUSED: counters[r * kvh + h] counts the finished partitions of a
+// multi-partition (row, KV head); the one that finishes last merges.
+template <int G, int WAVES, int PP, bool FUSED>
 __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, float* __restrict__ part,
     uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t row0, uint32_t qh, uint32_t kvh, uint32_t stride,
-    uint32_t pages, uint32_t context, uint32_t smax, uint32_t* err) {
-  constexpr uint32_t kWavePages = kAttnSplitPages / WAVES;
-  static_assert(kAttnSplitPages % WAVES == 0, "pages split evenly over the waves");
+    uint32_t pages, uint32_t context, uint32_t smax, uint32_t* counters, uint32_t* err) {
+  constexpr uint32_t kWavePages = PP / WAVES;
+  static_assert(PP % WAVES == 0 && kWavePages >= 1, "pages split evenly over the waves");
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
   // The wave index is uniform; saying so keeps every page address scalar.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t p0 = split * kAttnSplitPages;
+  const uint32_t p0 = split * PP;
   // This wave's pages: [w0, w0 + np) of the row. The page-table entries are
   // requested together with the position (they do not depend on it), so the
   // K loads wait for one memory round trip, not two.
@@ -98,7 +158,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   const uint32_t ctx = pos + 1;
   const uint32_t row_pages = (ctx + 15) / 16;
   if (p0 >= row_pages) return;  // uniform per workgroup
-  const uint32_t nsplit = (row_pages + kAttnSplitPages - 1) / kAttnSplitPages;
+  const uint32_t nsplit = (row_pages + PP - 1) / PP;
   const uint32_t np = w0 < row_pages ? min(row_pages - w0, kWavePages) : 0u;
 
   // Scores of the wave's tokens, replaced in place by probabilities: [token][g].
@@ -317,7 +377,37 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
           if (lw > 0.f) v += (c == 1 ? lw : wacc[w][g][c - 2]) * exp_fast(wstat[w][0][g] - M);
         }
       }
-      part[(((uint64_t)r * qh + h * G + g) * smax + split) * kAttnPartialFloats + c] = v;
+      float* dst = part + (((uint64_t)r * qh + h * G + g) * smax + split) * kAttnPartialFloats + c;
+      if constexpr (FUSED)
+        __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *dst = v;
+    }
+    if constexpr (FUSED) {
+      // The records are agent-scope atomic stores: the XCDs' L2 caches are
+      // not coherent with each other, and an agent-scope fence per workgroup
+      // (an L2 write-back and invalidate) costs more than the merge launch it
+      // would save. Each thread waits for its stores to complete, then the
+      // workgroup counts itself in; the workgroup that brings the count to
+      // nsplit merges the pair's G heads with agent-scope atomic loads (the
+      // merge kernel's code and order, so its outputs are the same).
+      __shared__ uint32_t last_s;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      uint32_t* counter = counters + (uint64_t)r * kvh + h;
+      if (threadIdx.x == 0) last_s = atomicAdd(counter, 1u) == nsplit - 1 ? 1u : 0u;
+      __syncthreads();
+      if (last_s) {
+        for (int g = wave; g < G; g += WAVES) {
+          float L, n0, n1;
+          merge_records<true>(part + ((uint64_t)r * qh + h * G + g) * smax * kAttnPartialFloats, nsplit, lane, L, n0,
+                              n1);
+          const uint32_t o0 = f32_to_bf16(n0 / L), o1 = f32_to_bf16(n1 / L);
+          bad |= !(L > 0.f) | ((o0 & 0x7f80u) == 0x7f80u) | ((o1 & 0x7f80u) == 0x7f80u);
+          store_head(out, out_mtiles, row0, r, qh, h * G + g, lane, o0, o1);
+        }
+        if (threadIdx.x == 0) atomicExch(counter, 0u);  // ready for the next launch
+      }
     }
   }
   if (bad) raise_error(err, ERR_NONFINITE);
@@ -328,7 +418,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
                                                                   const uint32_t* __restrict__ positions,
                                                                   uint16_t* __restrict__ out, uint32_t out_mtiles,
                                                                   uint32_t row0, uint32_t rows, uint32_t qh,
-                                                                  uint32_t context, uint32_t smax, uint32_t* err) {
+                                                                  uint32_t context, uint32_t smax,
+                                                                  uint32_t split_pages, uint32_t* err) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t id = blockIdx.x * 4 + wave;
   const uint32_t r = id / qh, head = id % qh;
@@ -336,55 +427,52 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
   const uint32_t pos = positions[r];
   if (pos >= context) return;  // reported by the partition kernel
   const uint32_t row_pages = (pos + 16) / 16;
-  const uint32_t ns = (row_pages + kAttnSplitPages - 1) / kAttnSplitPages;
+  const uint32_t ns = (row_pages + split_pages - 1) / split_pages;
   if (ns == 1) return;  // finished by the partition kernel
-  const float* p = part + ((uint64_t)r * qh + head) * smax * kAttnPartialFloats;
-  const float kNegInf = -__builtin_inff();
-  float mloc = kNegInf;
-  for (uint32_t sp = lane; sp < ns; sp += 64) mloc = fmaxf(mloc, p[(uint64_t)sp * kAttnPartialFloats]);
-  const float M = wave_max(mloc);
-  float L = 0.f, n0 = 0.f, n1 = 0.f;
-  for (uint32_t c0 = 0; c0 < ns; c0 += 64) {
-    // Lane s holds partition c0 + s's weight exp(m - M) and weighted l.
-    const uint32_t mine = c0 + lane;
-    const float ms = mine < ns ? p[(uint64_t)mine * kAttnPartialFloats] : kNegInf;
-    const float ws = mine < ns ? expf(ms - M) : 0.f;
-    const float lw = mine < ns ? p[(uint64_t)mine * kAttnPartialFloats + 1] * ws : 0.f;
-    const uint32_t cn = min(64u, ns - c0);
-    for (uint32_t s0 = 0; s0 < cn; s0 += 8) {
-      // Eight partitions' numerators in flight, then added in ascending order.
-      float a0[8], a1[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const uint32_t sp = s0 + u;
-        const float* ps = p + (uint64_t)(c0 + sp) * kAttnPartialFloats;
-        a0[u] = sp < cn ? ps[2 + 2 * lane] : 0.f;
-        a1[u] = sp < cn ? ps[3 + 2 * lane] : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const uint32_t sp = s0 + u;
-        if (sp < cn) {
-          const float w = lane_bcast(ws, (int)sp);
-          L += lane_bcast(lw, (int)sp);
-          n0 += a0[u] * w;
-          n1 += a1[u] * w;
-        }
-      }
-    }
-  }
+  float L, n0, n1;
+  merge_records(part + ((uint64_t)r * qh + head) * smax * kAttnPartialFloats, ns, lane, L, n0, n1);
   const uint32_t o0 = f32_to_bf16(n0 / L), o1 = f32_to_bf16(n1 / L);
   store_head(out, out_mtiles, row0, r, qh, head, lane, o0, o1);
   if (!(L > 0.f) || ((o0 & 0x7f80u) == 0x7f80u) || ((o1 & 0x7f80u) == 0x7f80u)) raise_error(err, ERR_NONFINITE);
 }
 
-template <int G, int WAVES = 8>
+template <int G, int PP, bool FUSED>
 void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                       const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
                       uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                      uint32_t smax, uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partition_kernel<G, WAVES>), dim3(smax, kvh, rows), dim3(64 * WAVES), 0, s, q, kc, vc,
-                     positions, table, part, out, out_mtiles, row0, qh, kvh, stride, pages, context, smax, err);
+                      uint32_t smax, uint32_t* counters, uint32_t* err, hipStream_t s) {
+  constexpr int kWaves = 8;
+  hipLaunchKernelGGL((attn_partition_kernel<G, kWaves, PP, FUSED>), dim3(smax, kvh, rows), dim3(64 * kWaves), 0, s,
+                     q, kc, vc, positions, table, part, out, out_mtiles, row0, qh, kvh, stride, pages, context, smax,
+                     counters, err);
+}
+
+template <int G, int PP>
+void launch_partition_pp(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
+                         const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
+                         uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                         uint32_t smax, uint32_t* counters, uint32_t* err, hipStream_t s) {
+  if (counters)
+    launch_partition<G, PP, true>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride,
+                                  pages, context, smax, counters, err, s);
+  else
+    launch_partition<G, PP, false>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride,
+                                   pages, context, smax, counters, err, s);
+}
+
+template <int G>
+hipError_t launch_partition_g(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
+                              const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
+                              uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
+                              uint32_t context, uint32_t split_pages, uint32_t* counters, uint32_t* err,
+                              hipStream_t s) {
+  const uint32_t smax = attn_max_splits(context, split_pages);
+  switch (split_pages) {
+    case 16: launch_partition_pp<G, 16>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, s); break;
+    case 32: launch_partition_pp<G, 32>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
 }
 
 }  // namespace
@@ -392,28 +480,30 @@ void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
                                     uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
-                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t* err,
-                                    hipStream_t s) {
-  const uint32_t smax = attn_max_splits(context);
+                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s) {
   const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
+  hipError_t e;
   switch (qh / kvh) {
-    case 1: launch_partition<1>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 2: launch_partition<2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 4: launch_partition<4>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
-    case 8: launch_partition<8>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, smax, err, s); break;
+    case 1: e = launch_partition_g<1>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
+    case 2: e = launch_partition_g<2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
+    case 4: e = launch_partition_g<4>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
+    case 8: e = launch_partition_g<8>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
     default: return hipErrorInvalidValue;
   }
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 
 hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
                                   uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
-                                  uint32_t context, uint32_t* err, hipStream_t s) {
-  const uint32_t smax = attn_max_splits(context);
+                                  uint32_t context, uint32_t split_pages, uint32_t* err, hipStream_t s) {
+  if (split_pages != 16 && split_pages != 32) return hipErrorInvalidValue;
+  const uint32_t smax = attn_max_splits(context, split_pages);
   const uint32_t waves = rows * qh;
   const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   hipLaunchKernelGGL(attn_merge_kernel, dim3((waves + 3) / 4), dim3(kAttnThreads), 0, s, partials, positions, out,
-                     mt, row0, rows, qh, context, smax, err);
+                     mt, row0, rows, qh, context, smax, split_pages, err);
   return hipGetLastError();
 }
 

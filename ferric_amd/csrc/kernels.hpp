@@ -12,10 +12,17 @@ namespace fh {
 // Records the message fh_last_error(NULL) returns on this thread.
 void set_thread_error(const char* msg);
 
-// Attention partition: each partition workgroup covers this many pages of
-// 16 tokens (its 8 waves take 4 pages each).
-constexpr uint32_t kAttnSplitPages = 32;
-constexpr uint32_t kAttnSplitTokens = kAttnSplitPages * 16;
+// Attention partitions: each partition workgroup covers split_pages pages of
+// 16 tokens (16 or 32; its 8 waves take split_pages / 8 pages each). Batches
+// of at most 64 (row, query head) pairs take 16-page partitions (measured on
+// MI355X, one Qwen3-8B row at a 4096-token context: 13.1 us against 15.7 us
+// for 32 pages, 15.2 us for 8; 4 rows: 32 pages best). attn_split_pages is
+// the one policy every launcher and workspace size uses.
+constexpr uint32_t kAttnMaxSplitPages = 32;
+constexpr uint32_t kAttnMinSplitPages = 16;
+inline uint32_t attn_split_pages(uint32_t rows, uint32_t query_heads) {
+  return (uint64_t)rows * query_heads <= 64 ? 16u : 32u;
+}
 // Floats per attention partial record: running max, denominator, numerator[128].
 constexpr uint32_t kAttnPartialFloats = 2 + 128;
 // Argmax first-pass shards per row.
@@ -31,8 +38,18 @@ __host__ __device__ inline uint32_t act_mtiles(uint32_t m) {
   return m <= kMaxRows ? 2u : ((m + kLargeBlockRows - 1) / kLargeBlockRows) * (kLargeBlockRows / 16);
 }
 
-inline uint32_t attn_max_splits(uint32_t context_tokens) {
-  return (context_tokens + kAttnSplitTokens - 1) / kAttnSplitTokens;
+inline uint32_t attn_max_splits(uint32_t context_tokens, uint32_t split_pages) {
+  return (context_tokens + split_pages * 16 - 1) / (split_pages * 16);
+}
+// Whether a decode launch merges its partitions in the partition kernel
+// (arrival counters) rather than in a second launch. Publishing the records
+// coherently adds a store and counter round trip to every partition
+// workgroup's life, which pays where the launch is small and costs where
+// it is large (measured on MI355X: 1 and 4 rows of Qwen3-8B 0.4-0.6 us
+// faster, 32 rows of Qwen3-0.6B at contexts U[128, 2048] even, 32 rows of
+// Qwen3-8B at U[512, 8192] 12 us slower).
+inline bool attn_fuse_merge(uint32_t rows, uint32_t kv_heads, uint32_t context_tokens, uint32_t split_pages) {
+  return (uint64_t)rows * kv_heads * attn_max_splits(context_tokens, split_pages) <= 2048;
 }
 
 // layout / data movement
@@ -92,14 +109,21 @@ uint32_t gemm_default_splits(uint32_t n, uint32_t k);
 // Rows [0, rows) of a launch are rows row0 + [0, rows) of an output of
 // out_rows rows (activation tile order with act_mtiles(out_rows) tiles when
 // out_tiled, else row-major); q/positions/table/partials are the launch's own.
+// Split-context decode attention with split_pages-page partitions (16 or
+// 32). partials holds rows x qh x attn_max_splits(context, split_pages)
+// records. Rows that fit one partition are finished by the partition launch.
+// counters == nullptr: multi-partition rows are finished by
+// launch_attention_merge (same split_pages). counters != nullptr: rows x kvh
+// words, zero on entry and left zero; the last partition of each (row, KV
+// head) to finish merges that pair's records itself, in the same launch.
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
                                     uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
-                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, uint32_t* err,
-                                    hipStream_t s);
+                                    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
+                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s);
 hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
                                   uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
-                                  uint32_t context, uint32_t* err, hipStream_t s);
+                                  uint32_t context, uint32_t split_pages, uint32_t* err, hipStream_t s);
 
 // Prefill attention over blocks of consecutive rows of one sequence (see
 // k_attention_block.hip). blocks[i] = first row | (rows << 16); each block

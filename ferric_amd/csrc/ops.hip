@@ -136,7 +136,7 @@ fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint1
 // copy, so calls that overlap on one GPU race; each call writes every record
 // it later reads, so nothing needs clearing between calls.
 namespace {
-constexpr uint64_t kNoAllocAttnRecords = 16384;  // rows x query heads x 512-token partitions (8.5 MB)
+constexpr uint64_t kNoAllocAttnRecords = 16384;  // rows x query heads x partitions (8.5 MB)
 constexpr int kNoAllocMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kNoAllocMaxDevices] = {};
@@ -188,10 +188,11 @@ fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cac
     return FH_ERR_INVALID_ARGUMENT;
   const uint32_t g = query_heads / kv_heads;
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
-  const uint64_t records = (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
+  const uint64_t records = (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens, split_pages);
   if (records > kNoAllocAttnRecords) {
-    fh::set_thread_error("fh_op_paged_attention_noalloc: rows x query_heads x ceil(context_tokens / 512) exceeds the "
-                         "16384 partition records of its static scratch");
+    fh::set_thread_error("fh_op_paged_attention_noalloc: rows x query_heads x partitions of the context exceeds "
+                         "the 16384 partition records of its static scratch");
     return FH_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = as_stream(stream);
@@ -200,15 +201,16 @@ fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cac
   (void)hipGetLastError();
   hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,
                                               rows, rows, query_heads, kv_heads, stride, physical_pages,
-                                              context_tokens, error_word, s);
+                                              context_tokens, split_pages, nullptr, error_word, s);
   if (e == hipSuccess)
     e = fh::launch_attention_merge(part, positions, out, out_tiled, 0, rows, rows, query_heads, context_tokens,
-                                   error_word, s);
+                                   split_pages, error_word, s);
   return status_of(e);
 }
 
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens) {
-  return (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens) * fh::kAttnPartialFloats * 4;
+  return (uint64_t)rows * query_heads *
+         fh::attn_max_splits(context_tokens, fh::attn_split_pages(rows, query_heads)) * fh::kAttnPartialFloats * 4;
 }
 
 fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -224,13 +226,14 @@ fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, cons
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
   hipStream_t s = as_stream(stream);
   float* part = reinterpret_cast<float*>(scratch);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
   (void)hipGetLastError();
   hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,
                                               rows, rows, query_heads, kv_heads, stride, physical_pages,
-                                              context_tokens, error_word, s);
+                                              context_tokens, split_pages, nullptr, error_word, s);
   if (e == hipSuccess)
     e = fh::launch_attention_merge(part, positions, out, out_tiled, 0, rows, rows, query_heads, context_tokens,
-                                   error_word, s);
+                                   split_pages, error_word, s);
   return status_of(e);
 }
 

@@ -80,6 +80,7 @@ struct fh_ctx {
   uint32_t s_qkv = 1, s_o = 1, s_down = 1;
   float* logits = nullptr;
   float* attn_part = nullptr;
+  uint32_t* attn_count = nullptr;  // [cap][kvh] partition arrival counters, zero between launches
   void* argmax_scratch = nullptr;
   uint32_t* choices = nullptr;
   uint32_t* err = nullptr;
@@ -393,6 +394,8 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   // `hidden` (one rounding, as the TP1 residual); the QKV partials are folded
   // by the QK-norm kernel.
   const uint32_t sq = ctx->s_qkv, so = ctx->s_o, sd = ctx->s_down;
+  const uint32_t split = fh::attn_split_pages(R, QH);
+  const bool fuse = fh::attn_fuse_merge(R, KVH, C, split);
   L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, ctx->hidden, R, H, md.vocabulary, err, s); });
   for (uint32_t l = 0; l < md.layers; ++l) {
@@ -419,11 +422,12 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
     });
     L(FH_KC_ATTENTION, [&] {
       return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, ctx->attn, 1, 0, R, R, QH,
-                                          KVH, stride, P, C, err, s);
+                                          KVH, stride, P, C, split, fuse ? ctx->attn_count : nullptr, err, s);
     });
-    L(FH_KC_ATTENTION_MERGE, [&] {
-      return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, 0, R, R, QH, C, err, s);
-    });
+    if (!fuse)
+      L(FH_KC_ATTENTION_MERGE, [&] {
+        return fh::launch_attention_merge(ctx->attn_part, d_pos, ctx->attn, 1, 0, R, R, QH, C, split, err, s);
+      });
     L(FH_KC_O_GEMM, [&] {
       return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, err, s);
     });
@@ -573,8 +577,10 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   TRY(dalloc(ctx, &ctx->o_part, (uint64_t)ctx->s_o * kMaxRows * H));
   TRY(dalloc(ctx, &ctx->down_part, (uint64_t)ctx->s_down * kMaxRows * H));
   TRY(dalloc(ctx, &ctx->logits, (uint64_t)cap * V));
-  TRY(dalloc(ctx, &ctx->attn_part,
-             (uint64_t)cap * md.query_heads * fh::attn_max_splits(op.context_tokens) * fh::kAttnPartialFloats));
+  TRY(dalloc(ctx, &ctx->attn_part, (uint64_t)cap * md.query_heads *
+                                        fh::attn_max_splits(op.context_tokens, fh::kAttnMinSplitPages) *
+                                        fh::kAttnPartialFloats));
+  TRY(dalloc(ctx, &ctx->attn_count, (uint64_t)cap * md.kv_heads));
   TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&ctx->argmax_scratch), fh_argmax_scratch_bytes(cap)));
   TRY(dalloc(ctx, &ctx->choices, cap));
   TRY(dalloc(ctx, &ctx->err, 64));
@@ -631,6 +637,8 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   // Deterministic contents for never-written KV slots and activations.
   e = fh::launch_fill_u16(ctx->kv, ctx->kv_slab_elems * 2 * md.layers, 0, ctx->stream);
   if (e == hipSuccess) e = fh::launch_fill_u16(ctx->hidden, (uint64_t)cap * H, 0, ctx->stream);
+  if (e == hipSuccess) e = fh::launch_fill_u16(reinterpret_cast<uint16_t*>(ctx->attn_count), 2ull * cap * md.kv_heads, 0,
+                                               ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return bail(hip_fail(ctx, e, "initialising the KV pool"));
 
@@ -1101,9 +1109,14 @@ fh_status fh_time_attention(fh_ctx* ctx, uint32_t reps, float* avg_ms) {
   const uint32_t* d_tab = ctx->d_meta + 2 * cap;
   hipStream_t s = ctx->stream;
   auto launch = [&] {
+    const uint32_t split = fh::attn_split_pages(R, md.query_heads);
+    const bool fuse = fh::attn_fuse_merge(R, md.kv_heads, op.context_tokens, split);
+    // The attention kernel class of the step: the partition launch (with the
+    // merge when the step fuses it; the merge launch is a class of its own).
     return fh::launch_attention_partial(ctx->qrot, kv_cache(ctx, l, 0), kv_cache(ctx, l, 1), d_pos, d_tab,
                                         ctx->attn_part, ctx->attn, 1, 0, R, R, md.query_heads, md.kv_heads,
-                                        op.page_table_stride, op.physical_pages, op.context_tokens, ctx->err, s);
+                                        op.page_table_stride, op.physical_pages, op.context_tokens, split,
+                                        fuse ? ctx->attn_count : nullptr, ctx->err, s);
   };
   hipEvent_t a = nullptr, b = nullptr;
   (void)hipGetLastError();

@@ -409,13 +409,19 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh, splits):
 
 
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
-@pytest.mark.parametrize("tiled,many", [(0, False), (1, False), (1, True)])
+@pytest.mark.parametrize("tiled,many", [(0, False), (1, False), (1, True), (0, None)])
 def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
-    r = rng(1000 + qh + 7 * many)
+    # Partition sizes follow the (rows x query heads) policy: 14 rows take
+    # 32-page (qh 32) or 16-page (qh 16) partitions, 40 rows 32-page ones, and
+    # 2 rows 8-page ones (up to 65 partitions per row: more than one 64-lane
+    # chunk of partition weights in the merge).
+    r = rng(1000 + qh + 7 * bool(many) + 13 * (many is None))
     pages, stride, context = 600, 520, 8320
     if many:
         # a prefill-size batch: 40 rows, tiled output of fh_activation_rows(40) rows
         positions = r.integers(0, 2000, 40).astype(np.uint32)
+    elif many is None:
+        positions = np.array([8319, 127], np.uint32)
     else:
         # one partition (<= 512 tokens), several partitions, page-boundary and partial-page cases
         positions = np.array([0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 8319, 77, 8190, 6000], np.uint32)
