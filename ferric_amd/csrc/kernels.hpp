@@ -44,12 +44,14 @@ inline uint32_t attn_max_splits(uint32_t context_tokens, uint32_t split_pages) {
 // Whether a decode launch merges its partitions in the partition kernel
 // (arrival counters) rather than in a second launch. Publishing the records
 // coherently adds a store and counter round trip to every partition
-// workgroup's life, which pays where the launch is small and costs where
-// it is large (measured on MI355X: 1 and 4 rows of Qwen3-8B 0.4-0.6 us
-// faster, 32 rows of Qwen3-0.6B at contexts U[128, 2048] even, 32 rows of
-// Qwen3-8B at U[512, 8192] 12 us slower).
+// workgroup's life, which pays where the launch is small and costs where it
+// is large. Measured on MI355X (alternating runs on one GPU, graph replays):
+// one Qwen3-8B row at a 4096-token context 3.555 against 3.635 ms per step
+// (16-page fused against 32-page separate merge); 32 rows of Qwen3-0.6B at
+// contexts U[128, 2048] (1280 partition workgroups) 2.136 against 2.122 ms;
+// 32 rows of Qwen3-8B at U[512, 8192] 12 us slower per launch fused.
 inline bool attn_fuse_merge(uint32_t rows, uint32_t kv_heads, uint32_t context_tokens, uint32_t split_pages) {
-  return (uint64_t)rows * kv_heads * attn_max_splits(context_tokens, split_pages) <= 2048;
+  return (uint64_t)rows * kv_heads * attn_max_splits(context_tokens, split_pages) <= 1024;
 }
 
 // layout / data movement
