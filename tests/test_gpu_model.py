@@ -629,49 +629,64 @@ class ParityRunner:
         return out
 
 
-@pytest.mark.parametrize("same_draft", [True, False])
-def test_speculative_rounds_match_the_oracle(same_draft):
-    # Greedy speculation (K = 4, 8 sequences) of a 2-layer 0.6B-shaped draft
-    # for a 2-layer 0.6B-shaped target, every draft step, catch-up and verify
-    # batch run on the GPU and on the oracle in lockstep. With identical
-    # weights the draft is mostly accepted (every full acceptance exercises
-    # the draft catch-up); with other weights mostly rejected. Then: each
-    # round's 120-byte completion records equal the oracle's records built
-    # from the same round's choices, and both models' KV pools hold, in every
-    # slot the rounds wrote (accepted and rejected suffixes alike), the
-    # oracle's K/V; nothing else changed.
+SPEC_SHAPES = {
+    # name: (target config, draft config, same weights, sequences, rounds)
+    "0.6b-same-draft": (dict(ferric_amd.QWEN3_0_6B, layers=2), dict(ferric_amd.QWEN3_0_6B, layers=2), True, 8, 4),
+    "0.6b-other-draft": (dict(ferric_amd.QWEN3_0_6B, layers=2), dict(ferric_amd.QWEN3_0_6B, layers=2), False, 8, 4),
+    # the speculative benchmark's geometry with 2 layers each: an 8B-shaped
+    # target (untied head) and a 0.6B-shaped draft (tied head), 32
+    # sequences, so every verify is a 160-row batch
+    "8b-target-0.6b-draft": (dict(ferric_amd.QWEN3_8B, layers=2), dict(ferric_amd.QWEN3_0_6B, layers=2), False, 32, 2),
+}
+
+
+@pytest.mark.parametrize("shape", list(SPEC_SHAPES))
+def test_speculative_rounds_match_the_oracle(shape):
+    # Greedy speculation (K = 4), every draft step, catch-up and verify batch
+    # run on the GPU and on the oracle in lockstep. With identical weights the
+    # draft is mostly accepted (every full acceptance exercises the draft
+    # catch-up); with other weights mostly rejected. Then: each round's
+    # 120-byte completion records equal the oracle's records built from the
+    # same round's choices, and both models' KV pools hold, in every slot the
+    # rounds wrote (accepted and rejected suffixes alike), the oracle's K/V;
+    # nothing else changed.
     from ferric_amd.speculative import SpeculativeDecoder
 
-    cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
+    cfg_t, cfg_d, same_draft, nseq, rounds = SPEC_SHAPES[shape]
+    K = 4
     limits = PagedLimits(context_tokens=256, physical_page_count=160, page_table_stride=16)
-    tp = Pair(cfg, limits, seed=5, capture=False, rows=16, prefill_rows=128)
-    dp = Pair(cfg, limits, seed=5 if same_draft else 6, capture=False, rows=16, prefill_rows=128)
+    rng = np.random.default_rng(77)
+    lengths = (3, 9, 16, 5, 7, 12, 2, 20) if nseq == 8 else tuple(int(n) for n in rng.integers(1, 5, nseq))
+    prompts = [list(rng.integers(0, cfg_t["vocabulary"], n)) for n in lengths]
+    rows = 32 if nseq > 16 else 16
+    prefill = max(sum(lengths), nseq * (K + 1))  # the prompt batch and every verify batch
+    tp = Pair(cfg_t, limits, seed=5, capture=False, rows=rows, prefill_rows=prefill)
+    dp = Pair(cfg_d, limits, seed=5 if same_draft else 6, capture=False, rows=rows, prefill_rows=prefill)
     try:
         target, draft = ParityRunner(tp, "target"), ParityRunner(dp, "draft")
-        rng = np.random.default_rng(77)
-        prompts = [list(rng.integers(0, cfg["vocabulary"], n)) for n in (3, 9, 16, 5, 7, 12, 2, 20)]
-        dec = SpeculativeDecoder(target, tp.pool, draft, dp.pool, k=4)
-        dec.prefill(prompts)  # 74 prompt rows: the prefill path for both models
+        dec = SpeculativeDecoder(target, tp.pool, draft, dp.pool, k=K)
+        dec.prefill(prompts)  # the prefill path for both models
         accepted = 0
-        for rnd in range(4):
+        for rnd in range(rounds):
             draft_steps_before = draft.batches
-            st = dec.round()  # the verify batch has 8 x 5 = 40 rows: the prefill path
+            st = dec.round()  # verify batch of nseq x (K + 1) rows: the prefill path
+            assert st.target_rows == nseq * (K + 1)
             accepted += sum(st.accepted)
-            assert draft.batches - draft_steps_before in (4, 5)  # K steps, plus a catch-up after a full accept
+            assert draft.batches - draft_steps_before in (K, K + 1)  # K steps, plus a catch-up after a full accept
             # the GPU's verify choices are the oracle's (checked in ParityRunner, up to near-ties)
             gpu_choices = np.asarray(st.target_choices, np.uint32)
             if not target.flips:
                 assert gpu_choices.reshape(-1).tolist() == target.last_ref["choices"]
             # each record is the oracle's restatement of the reference's record for the round's choices
             for j, rec in enumerate(st.records):
-                want, _ = orc.compact_record(gpu_choices, st.draft, 5, j, 1, rnd, dec.plan, len(prompts), j, 5,
-                                             dec.k)
+                want, _ = orc.compact_record(gpu_choices, st.draft, K + 1, j, 1, rnd, dec.plan, len(prompts), j,
+                                             K + 1, dec.k)
                 assert rec == want, (rnd, j)
                 assert rec[48] == st.accepted[j] and rec[49] == len(st.emitted[j])
-        print(f"accepted {accepted} of {4 * 4 * len(prompts)} draft tokens; flips target {target.flips} "
+        print(f"accepted {accepted} of {rounds * K * len(prompts)} draft tokens; flips target {target.flips} "
               f"draft {draft.flips}; worst logit err target {target.worst_logit:.2e} draft {draft.worst_logit:.2e}")
         if same_draft:
-            assert accepted >= 4 * 4 * len(prompts) // 2
+            assert accepted >= rounds * K * len(prompts) // 2
         tp.check_kv()
         dp.check_kv()
     finally:
