@@ -299,7 +299,7 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint32_t row = mt0 * 16 + lane;
     if (row < m)
-      qknorm_rope_kv_head<32>(reinterpret_cast<const qk_u32x4*>(rows_lds + lane * kQkPitch), row,
+      qknorm_rope_kv_head<32, true>(reinterpret_cast<const qk_u32x4*>(rows_lds + lane * kQkPitch), row,
                               blockIdx.x * 2 + wn, qa, row_slot);
     return;
   }

@@ -80,7 +80,9 @@ __device__ __forceinline__ QkvRowSlot qkv_row_slot(uint32_t row, const QkvRopeAr
 // rotated) and value heads (raw) to the row's KV slot. kHoist: cos/sin pairs
 // requested at a time (8 keeps the lane-per-head kernel's registers low
 // enough for its occupancy; a caller with few waves takes all 32 at once).
-template <int kHoist = 8>
+// kHwCvt: narrow with the conversion instruction (equal results, far fewer
+// instructions) where the caller has the registers for it.
+template <int kHoist = 8, bool kHwCvt = false>
 __device__ __forceinline__ void qknorm_rope_kv_head(const qk_u32x4* src, uint32_t row, uint32_t head,
                                                     const QkvRopeArgs& a, const QkvRowSlot rs) {
   uint32_t x[64];  // x[i] = elements 2 i (low half) and 2 i + 1 (high half)
@@ -128,8 +130,10 @@ __device__ __forceinline__ void qknorm_rope_kv_head(const qk_u32x4* src, uint32_
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t xi = x[4 * i + j];
-      const uint32_t lo = norm_weight_bf16_int(lo_bf16(xi), inv, lo_bf16(w[j]));
-      const uint32_t hi = norm_weight_bf16_int(hi_bf16(xi), inv, hi_bf16(w[j]));
+      const uint32_t lo = kHwCvt ? norm_weight_bf16(lo_bf16(xi), inv, lo_bf16(w[j]))
+                                 : norm_weight_bf16_int(lo_bf16(xi), inv, lo_bf16(w[j]));
+      const uint32_t hi = kHwCvt ? norm_weight_bf16(hi_bf16(xi), inv, hi_bf16(w[j]))
+                                 : norm_weight_bf16_int(hi_bf16(xi), inv, hi_bf16(w[j]));
       x[4 * i + j] = lo | (hi << 16);
     }
   }
@@ -144,8 +148,10 @@ __device__ __forceinline__ void qknorm_rope_kv_head(const qk_u32x4* src, uint32_
     const float b0 = lo_bf16(x[i + 32]), b1 = hi_bf16(x[i + 32]);
     const float a0c = a0 * c.x, b0s = b0 * sn.x, b0c = b0 * c.x, a0s = a0 * sn.x;
     const float a1c = a1 * c.y, b1s = b1 * sn.y, b1c = b1 * c.y, a1s = a1 * sn.y;
-    const uint32_t ra0 = f32_to_bf16_int(a0c - b0s), rb0 = f32_to_bf16_int(b0c + a0s);
-    const uint32_t ra1 = f32_to_bf16_int(a1c - b1s), rb1 = f32_to_bf16_int(b1c + a1s);
+    const uint32_t ra0 = kHwCvt ? f32_to_bf16(a0c - b0s) : f32_to_bf16_int(a0c - b0s);
+    const uint32_t rb0 = kHwCvt ? f32_to_bf16(b0c + a0s) : f32_to_bf16_int(b0c + a0s);
+    const uint32_t ra1 = kHwCvt ? f32_to_bf16(a1c - b1s) : f32_to_bf16_int(a1c - b1s);
+    const uint32_t rb1 = kHwCvt ? f32_to_bf16(b1c + a1s) : f32_to_bf16_int(b1c + a1s);
     bad |= ((ra0 & 0x7f80u) == 0x7f80u) | ((rb0 & 0x7f80u) == 0x7f80u) | ((ra1 & 0x7f80u) == 0x7f80u) |
            ((rb1 & 0x7f80u) == 0x7f80u);
     x[i] = ra0 | (ra1 << 16);
