@@ -328,7 +328,8 @@ __global__ __launch_bounds__(256, 2) void qknorm_rope_kv_rows_kernel(const uint1
 // different waves would cost partial-line writes). All of a thread's
 // chunks belong to row t % 16: the row's sum of squares is the thread
 // partials (chunks in ascending j) added over t = r, r + 16, ... in order.
-// width % 32 == 0, width <= 4096.
+// The norm weight is staged in LDS with the row loads, so the output pass
+// waits for no second memory round trip. width % 32 == 0, width <= 4096.
 constexpr uint32_t kTileRows = 16;
 constexpr int kTileThreads = 512;
 constexpr int kRowsMaxChunks = 4096 / 8 * kTileRows / kTileThreads;  // 16
@@ -341,11 +342,13 @@ __global__ __launch_bounds__(kTileThreads) void rmsnorm_tile_rows_kernel(const u
   __shared__ float part[kTileThreads];
   __shared__ float inv_s[kTileRows];
   __shared__ uint32_t bad_s;
+  __shared__ uint4 w_s[4096 / 8];
   const uint32_t t = threadIdx.x, mt = blockIdx.x, row0 = mt * kTileRows;
   const uint32_t lane = t & 63u, r = lane & 15u, g = lane >> 4;
   const uint32_t kbs = width / 32;  // k-blocks per row
   const bool live = row0 + r < rows;
   if (t == 0) bad_s = 0;
+  for (uint32_t c = t; c < width / 8; c += kTileThreads) w_s[c] = *reinterpret_cast<const uint4*>(w + c * 8);
   uint4 v[kRowsMaxChunks];
   float sum = 0.f;
 #pragma unroll
@@ -382,7 +385,7 @@ __global__ __launch_bounds__(kTileThreads) void rmsnorm_tile_rows_kernel(const u
     if (kb < kbs) {
       uint32_t o[4] = {0u, 0u, 0u, 0u};
       if (live) {
-        const uint4 wv = *reinterpret_cast<const uint4*>(w + kb * 32 + g * 8);
+        const uint4 wv = w_s[kb * 4 + g];
         const uint32_t xs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
         const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
