@@ -92,7 +92,11 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 4}), flush=True)
 
 
-ATTN_PARTITION_TOKENS = 512  # 32 pages of 16 tokens per attention partition
+def attn_partition_tokens(rows, query_heads):
+    """Tokens per decode attention partition: 32 pages of 16, or 16 pages
+    when the launch has at most 64 (row, query head) pairs (the library's
+    attn_split_pages)."""
+    return 256 if rows * query_heads <= 64 else 512
 
 
 def kernel_bytes(cfg, rows, positions, stride):
@@ -102,9 +106,10 @@ def kernel_bytes(cfg, rows, positions, stride):
     nqkv = Q + 2 * KV
     ctx = np.asarray(positions, np.int64) + 1
     kv_read = int(np.sum(ctx)) * KV * 2 * 2  # K and V rows, bf16
-    # Rows longer than one 512-token partition leave one FP32 record
-    # (max, denominator, 128 numerators) per query head and partition.
-    parts = (ctx + ATTN_PARTITION_TOKENS - 1) // ATTN_PARTITION_TOKENS
+    # Rows longer than one partition leave one FP32 record (max, denominator,
+    # 128 numerators) per query head and partition.
+    tokens = attn_partition_tokens(rows, QH)
+    parts = (ctx + tokens - 1) // tokens
     merge_read = int(np.sum(np.where(parts > 1, parts, 0))) * QH * 130 * 4
     merged_rows = int(np.sum(parts > 1))
     return {
