@@ -400,11 +400,13 @@ def main():
 
     step_positions = []
     device_ms = 0.0
+    step_device_ms = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tokens, positions = step(tokens)
-        device_ms += runner.last_step_ms()
+        step_device_ms.append(runner.last_step_ms())
+        device_ms += step_device_ms[-1]
         step_positions.append(positions)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -450,6 +452,7 @@ def main():
                    "decode_steps_timed": args.steps, "page_tokens": 16, "physical_pages": phys_pages,
                    "graphs": not args.eager, "profile_steps": args.profile_steps},
         "device_ms_per_step": round(device_ms / args.steps, 4),  # HIP events around each step on the stream
+        "device_ms_median": round(float(np.median(step_device_ms)), 4),
         "step_hbm": {"achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(step_gbs / PEAK_HBM_GBS, 4),
                      "bytes_per_step": int(step_byte_total / args.steps)},
