@@ -316,6 +316,32 @@ def test_qwen3_8b_layer_shapes_match_oracle():
         pair.close()
 
 
+def test_small_batches_merge_attention_partitions_in_kernel():
+    # Launches of at most 1024 partition workgroups merge their attention
+    # partitions in the partition kernel (the last partition of each (row, KV
+    # head) to finish). A 2-layer 8B-shaped model, two steps each, graph path,
+    # against the oracle: one row at a 30000-token context (16-page
+    # partitions, 118 of them: more than one 64-lane chunk of partition
+    # weights in the merge), and four rows at up to 8000 tokens (32-page
+    # partitions, several rows per launch).
+    cfg = dict(ferric_amd.QWEN3_8B, layers=2)
+    cases = [([30000], PagedLimits(context_tokens=30080, physical_page_count=2000, page_table_stride=1880)),
+             ([8000, 5003, 700, 3001], PagedLimits(context_tokens=8192, physical_page_count=1200, page_table_stride=512))]
+    for lengths, limits in cases:
+        pair = Pair(cfg, limits, seed=23, rows=len(lengths), graphs=True)
+        try:
+            sids = pair.admit_with_prefix(lengths)
+            toks = [int(t) for t in np.random.default_rng(len(lengths)).integers(0, cfg["vocabulary"], len(sids))]
+            for step in range(2):
+                batch, out, ref = pair.step(list(zip(sids, toks)))
+                _mark_written(pair, batch)
+                pair.check(batch, out, ref, f"{len(lengths)} rows step {step}")
+                toks = [int(c) for c in ref["choices"]]
+            pair.check_kv()
+        finally:
+            pair.close()
+
+
 GOLDEN_SPREAD = Path(__file__).resolve().parent / "golden" / "reduction_spread.json"
 
 
