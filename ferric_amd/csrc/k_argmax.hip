@@ -75,27 +75,40 @@ __global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(const float
 
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pval,
                                                           const uint32_t* __restrict__ pidx,
-                                                          uint32_t* __restrict__ choices, uint32_t* err) {
+                                                          uint32_t* __restrict__ choices, uint32_t* err,
+                                                          uint32_t* host_choices, uint32_t* host_err) {
   const uint32_t row = blockIdx.x;
   Cand c{pval[row * kArgmaxShards + threadIdx.x], pidx[row * kArgmaxShards + threadIdx.x]};
   c = wave_best(c);
   if (threadIdx.x == 0) {
-    choices[row] = c.id == kNone ? 0u : c.id;
+    const uint32_t id = c.id == kNone ? 0u : c.id;
+    choices[row] = id;
     if (c.id == kNone) raise_error(err, ERR_NONFINITE);
+    if (host_choices) {
+      __hip_atomic_store(host_choices + row, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (row == 0) {
+        // Every earlier launch has completed, and a row with no finite logit
+        // raised ERR_NONFINITE in the partial pass already, so the word read
+        // here holds every error bit the step can report.
+        const uint32_t e = err ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        __hip_atomic_store(host_err, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+    }
   }
 }
 
 }  // namespace
 
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
-                         uint32_t* err, hipStream_t s) {
+                         uint32_t* err, hipStream_t s, uint32_t* host_choices, uint32_t* host_err) {
   float* pval = reinterpret_cast<float*>(scratch);
   uint32_t* pidx = reinterpret_cast<uint32_t*>(pval + (uint64_t)rows * kArgmaxShards);
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxShards, rows), dim3(kArgThreads), 0, s, logits, vocab, pval,
                      pidx, err);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, pval, pidx, choices, err);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, pval, pidx, choices, err,
+                     host_choices, host_err);
   return hipGetLastError();
 }
 

@@ -148,6 +148,17 @@ __global__ void clear_word_kernel(uint32_t* word) {
   if (threadIdx.x == 0) *word = 0u;
 }
 
+// System-scope loads read the coherent pinned buffer past every GPU cache, so
+// each step sees what the host wrote before the launch.
+__global__ __launch_bounds__(kThreads) void step_ingest_kernel(const uint32_t* __restrict__ host,
+                                                               uint32_t* __restrict__ dev, uint32_t words,
+                                                               uint32_t* err) {
+  if (blockIdx.x == 0 && threadIdx.x == 0 && err) *err = 0u;
+  uint32_t* src = const_cast<uint32_t*>(host);
+  for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < words; i += gridDim.x * kThreads)
+    dev[i] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __global__ __launch_bounds__(kThreads) void copy_u16_kernel(const uint16_t* __restrict__ src,
                                                             uint16_t* __restrict__ dst, uint64_t count) {
   const uint64_t chunks = count / 8;
@@ -207,6 +218,12 @@ hipError_t launch_gather_rows(const uint16_t* src, const uint32_t* index, uint16
 
 hipError_t launch_clear_word(uint32_t* word, hipStream_t s) {
   hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(64), 0, s, word);
+  return hipGetLastError();
+}
+
+hipError_t launch_step_ingest(const uint32_t* host, uint32_t* dev, uint32_t words, uint32_t* err, hipStream_t s) {
+  hipLaunchKernelGGL(step_ingest_kernel, dim3(grid_for(words, kThreads, 256)), dim3(kThreads), 0, s, host, dev, words,
+                     err);
   return hipGetLastError();
 }
 

@@ -69,6 +69,10 @@ hipError_t launch_kv_fill(uint16_t* cache, const uint32_t* table, const uint32_t
 hipError_t launch_gather_rows(const uint16_t* src, const uint32_t* index, uint16_t* dst, uint32_t rows,
                               uint32_t width, hipStream_t s);
 hipError_t launch_clear_word(uint32_t* word, hipStream_t s);
+// The first launch of a decode step: copies `words` 32-bit words of step
+// metadata from coherent pinned host memory to device memory and clears the
+// error word, in place of a host-to-device copy and a clear.
+hipError_t launch_step_ingest(const uint32_t* host, uint32_t* dev, uint32_t words, uint32_t* err, hipStream_t s);
 hipError_t launch_copy_u16(const uint16_t* src, uint16_t* dst, uint64_t count, hipStream_t s);
 
 // norms / activation
@@ -139,7 +143,10 @@ hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, c
                                    uint32_t* err, hipStream_t s);
 
 // logits
+// With host_choices (coherent pinned memory), the choices and the error word
+// (at host_err) are also stored there, so the host reads them after the
+// stream synchronizes without a device-to-host copy.
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
-                         uint32_t* err, hipStream_t s);
+                         uint32_t* err, hipStream_t s, uint32_t* host_choices = nullptr, uint32_t* host_err = nullptr);
 
 }  // namespace fh
