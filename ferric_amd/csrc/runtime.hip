@@ -135,11 +135,18 @@ struct fh_ctx {
   uint32_t class_launches[FH_KC_COUNT] = {};
 
   // Validation scratch (stamped arrays, sized by physical_pages).
-  std::vector<uint64_t> page_stamp;
-  std::vector<uint64_t> page_seq;
-  std::vector<uint32_t> page_logical;
-  std::vector<uint8_t> page_conflict;
-  std::vector<uint64_t> row_stamp;
+  // Batch validation: per physical page, the batch that last listed it
+  // (stamp), the owner (sequence, logical index) that batch gave it, whether
+  // two owners disagree, and the last row that listed it.
+  struct PageOwner {
+    uint64_t stamp = 0;
+    uint64_t sequence = 0;
+    uint32_t logical = 0;
+    uint32_t row = 0;
+    uint32_t conflict = 0;
+  };
+  std::vector<PageOwner> page_owner;
+  std::vector<uint8_t> row_dup;  // per row of the batch: a page listed twice
   std::vector<uint64_t> slot_scratch;
   uint64_t stamp = 0;
 };
@@ -290,25 +297,35 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
     return fail(ctx, FH_ERR_OUTPUT_ROWS, "output rows must be unique, ascending, and within the batch");
   const uint32_t P = ctx->opt.physical_pages, stride = ctx->opt.page_table_stride;
   const uint64_t gen = ++ctx->stamp;
-  // Pass 1: page -> (sequence, logical) ownership over every row's list.
+  // Pass 1, one visit per listed page: page -> (sequence, logical) ownership
+  // over every row's list, and whether a row lists a page twice (the page's
+  // last listing row is this row already).
+  std::vector<uint8_t>& dup = ctx->row_dup;
+  dup.assign(nrows, 0);
+  fh_ctx::PageOwner* owner = ctx->page_owner.data();
   for (uint32_t i = 0; i < nrows; ++i) {
     const fh_row& r = rows[i];
     if (r.page_count > stride || (r.page_count && r.pages == nullptr))
       return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
+    uint8_t row_dup = 0;
     for (uint32_t j = 0; j < r.page_count; ++j) {
       const uint32_t pg = r.pages[j];
       if (pg >= P) return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
-      if (ctx->page_stamp[pg] != gen) {
-        ctx->page_stamp[pg] = gen;
-        ctx->page_seq[pg] = r.sequence;
-        ctx->page_logical[pg] = j;
-        ctx->page_conflict[pg] = 0;
-      } else if (ctx->page_seq[pg] != r.sequence || ctx->page_logical[pg] != j) {
-        ctx->page_conflict[pg] = 1;
+      fh_ctx::PageOwner& o = owner[pg];
+      if (o.stamp != gen) {
+        o.stamp = gen;
+        o.sequence = r.sequence;
+        o.logical = j;
+        o.conflict = 0;
+      } else {
+        row_dup |= o.row == i;
+        if (o.sequence != r.sequence || o.logical != j) o.conflict = 1;
       }
+      o.row = i;
     }
+    dup[i] = row_dup;
   }
-  // Pass 2: per-row geometry, unique pages, unique write slots.
+  // Pass 2, per row in order: geometry, unique pages, unique write slots.
   std::vector<uint64_t>& slots = ctx->slot_scratch;
   slots.clear();
   for (uint32_t i = 0; i < nrows; ++i) {
@@ -317,16 +334,10 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
     if (r.position >= ctx->opt.context_tokens || r.token >= ctx->md.vocabulary || logical >= r.page_count ||
         r.pages[logical] != r.writable_page)
       return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
-    const uint64_t row_gen = (gen << 16) | i;  // i < 16384
-    for (uint32_t j = 0; j < r.page_count; ++j) {
-      const uint32_t pg = r.pages[j];
-      if (ctx->row_stamp[pg] == row_gen)
-        return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
-      ctx->row_stamp[pg] = row_gen;
-    }
+    if (dup[i]) return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
     slots.push_back((uint64_t)r.pages[logical] * kPageTokens + r.position % kPageTokens);
-    const uint32_t wp = r.pages[logical];
-    if (ctx->page_conflict[wp] || ctx->page_seq[wp] != r.sequence || ctx->page_logical[wp] != logical)
+    const fh_ctx::PageOwner& o = owner[r.pages[logical]];
+    if (o.conflict || o.sequence != r.sequence || o.logical != logical)
       return fail(ctx, FH_ERR_SHARED_PAGE, "batch writes a page shared with another sequence or logical position");
   }
   std::sort(slots.begin(), slots.end());
@@ -648,11 +659,7 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return bail(hip_fail(ctx, e, "initialising the KV pool"));
 
-  ctx->page_stamp.assign(op.physical_pages, 0);
-  ctx->page_seq.assign(op.physical_pages, 0);
-  ctx->page_logical.assign(op.physical_pages, 0);
-  ctx->page_conflict.assign(op.physical_pages, 0);
-  ctx->row_stamp.assign(op.physical_pages, 0);
+  ctx->page_owner.assign(op.physical_pages, fh_ctx::PageOwner{});
 #undef TRY
   *out = ctx;
   return FH_OK;

@@ -27,14 +27,16 @@ class SequenceState:
         self.length = 0  # committed tokens (KV positions 0..length-1 are written)
         self._table = np.zeros(capacity, dtype=np.uint32)
         self._count = 0
+        self._view = self._table[:0]  # the reserved pages, re-sliced only when one is added
 
     @property
     def pages(self) -> np.ndarray:
-        return self._table[: self._count]
+        return self._view
 
     def append_page(self, page: int) -> None:
         self._table[self._count] = page
         self._count += 1
+        self._view = self._table[: self._count]
 
 
 class PagePool:
@@ -78,11 +80,11 @@ class PagePool:
         else:
             cols = self._prepare_vector(rows)
         states, sid, token, pos, group = cols
-        lens = np.array([st._count for st in states], dtype=np.int64)
+        lens = np.fromiter([st._count for st in states], dtype=np.int64, count=len(states))
         offs = np.zeros(len(states), dtype=np.int64)
         if len(states) > 1:
-            offs[1:] = np.cumsum(lens[:-1])
-        tables = np.concatenate([st.pages for st in states]) if states else np.zeros(0, np.uint32)
+            np.cumsum(lens[:-1], out=offs[1:])
+        tables = np.concatenate([st._view for st in states]) if states else np.zeros(0, np.uint32)
         writable = tables[offs[group] + pos // PAGE_TOKENS] if len(token) else np.zeros(0, np.uint32)
         prepared = PreparedRows(sid, token, pos, writable, tables, offs, lens, group)
         bid = self._next_batch
@@ -90,26 +92,30 @@ class PagePool:
         return PreparedBatch(bid, prepared, self.limits)
 
     def _prepare_loop(self, rows: list):
+        sequences = self.sequences
         group_of: dict[int, int] = {}
-        states, pending = [], []
+        states, next_pos = [], []  # per sequence, in order of first appearance
         sid, token, pos, group = [], [], [], []
         for s, t in rows:
             g = group_of.get(s)
             if g is None:
                 g = group_of[s] = len(states)
-                states.append(self.sequences[s])
-                pending.append(0)
-            st = states[g]
-            p = st.length + pending[g]
-            pending[g] += 1
+                st = sequences[s]
+                states.append(st)
+                next_pos.append(st.length)
+            else:
+                st = states[g]
+            p = next_pos[g]
+            next_pos[g] = p + 1
             if p // PAGE_TOKENS >= st._count:
                 self._ensure(st, p + 1)
             sid.append(s)
             token.append(int(t))
             pos.append(p)
             group.append(g)
-        return (states, np.array(sid, dtype=np.int64), np.array(token, dtype=np.int64),
-                np.array(pos, dtype=np.int64), np.array(group, dtype=np.int64))
+        n = len(rows)
+        return (states, np.fromiter(sid, dtype=np.int64, count=n), np.fromiter(token, dtype=np.int64, count=n),
+                np.fromiter(pos, dtype=np.int64, count=n), np.fromiter(group, dtype=np.int64, count=n))
 
     def _prepare_vector(self, rows: list):
         n = len(rows)

@@ -468,6 +468,43 @@ def test_batch_validation_mirrors_the_reference():
         r.close()
 
 
+@pytest.mark.parametrize("graphs", [True, False])
+def test_device_error_of_a_decode_step_reaches_the_host(graphs):
+    # A decode step's error word and choices come back through pinned host
+    # memory that the step's last launch writes. A NaN planted in the final
+    # norm makes every logit nonfinite: the step (a replay of the graph the
+    # good steps captured, or eager launches) must fail with
+    # FH_ERR_NONFINITE, and the runner then refuses further steps.
+    from ferric_amd import _lib
+    from ferric_amd.checkpoint import NO_LAYER
+
+    cfg = dict(ferric_amd.QWEN3_0_6B, layers=1)
+    limits = PagedLimits(context_tokens=256, physical_page_count=32, page_table_stride=16)
+    r = TpBatchRunner(cfg, limits, row_capacity=4, use_graphs=graphs)
+    try:
+        r.synthesize_weights(3, 0.02)
+        pool = PagePool(limits, seed=3)
+        sids = [pool.admit(0), pool.admit(0)]
+        toks = [11, 12]
+        for _ in range(3):
+            b = pool.prepare(list(zip(sids, toks)))
+            toks = r.execute_batch(b, [0, 1]).choices
+            pool.commit(b)
+            assert all(0 <= t < cfg["vocabulary"] for t in toks)
+        norm = r.download_weight(_lib.FINAL_NORM, NO_LAYER, cfg["hidden"])
+        norm[17] = 0x7FC0
+        r.upload_weight(_lib.FINAL_NORM, NO_LAYER, norm)
+        b = pool.prepare(list(zip(sids, toks)))
+        with pytest.raises(FerricError) as e:
+            r.execute_batch(b, [0, 1])
+        assert e.value.status == 6, e.value
+        with pytest.raises(FerricError) as e:
+            r.execute_batch(pool.prepare(list(zip(sids, toks))), [0, 1])
+        assert e.value.status == 8, e.value
+    finally:
+        r.close()
+
+
 def test_full_small_model_prompt_then_greedy_decode():
     # Qwen3-0.6B shape, all 28 layers, batch 1: a 16-token prompt as one
     # 16-row batch, then 8 greedy decode steps (teacher-forced).
