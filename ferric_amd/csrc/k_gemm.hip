@@ -38,9 +38,8 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// blockIdx.z selects a 32-row chunk of the activation (rows 32 z ..), for
-// batches of more than 32 rows: every chunk streams the same weight tiles,
-// which the chip's caches serve to the chunks' concurrent workgroups.
+// Batches of more than 32 rows run as 32-row chunks (gridDim.z of them, one
+// split): every chunk streams the same weight tiles.
 template <int NT, int MT, int EPI, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __restrict__ xt,
                                                          const uint16_t* __restrict__ w, uint32_t m_total,
@@ -49,7 +48,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
                                                          uint32_t* err) {
   __shared__ float red[WAVES][NT * MT * 256];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t tile0 = blockIdx.x * NT;
+  // A launch over several 32-row chunks (always one split) reads each weight
+  // slice once per chunk. Workgroups go to the 8 XCDs round-robin by
+  // dispatch order, so the order is arranged for the chunks of one slice to
+  // be dispatched back to back on one XCD: they run together there and the
+  // later ones find the weight tiles in that XCD's L2. Slices past the last
+  // multiple of 8 keep their chunks consecutive in dispatch order.
+  uint32_t slice = blockIdx.x, chunk = blockIdx.z;
+  if (gridDim.z > 1) {
+    const uint32_t S = gridDim.x, C = gridDim.z, S8 = S & ~7u;
+    const uint32_t b = blockIdx.x + S * blockIdx.z;
+    if (b < S8 * C) {
+      const uint32_t r = b >> 3;
+      chunk = r % C;
+      slice = (r / C) * 8 + (b & 7u);
+    } else {
+      const uint32_t t = b - S8 * C;
+      slice = S8 + t / C;
+      chunk = t % C;
+    }
+  }
+  const uint32_t tile0 = slice * NT;
   const uint32_t split = blockIdx.y;
   const uint32_t s_lo = split * kb_split;
   const uint32_t s_hi = min(s_lo + kb_split, kb_count);
@@ -61,10 +80,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     wp[nt] = reinterpret_cast<const u32x4*>(w) + ((uint64_t)(tile0 + nt) * kb_count + kb_lo) * 64 + lane;
-  const uint32_t row0 = blockIdx.z * 32;
-  const uint32_t m = min(m_total - row0, 32u);
+  const uint32_t row0 = chunk * 16 * MT;
+  const uint32_t m = min(m_total - row0, 16u * MT);
   const uint64_t xkb = (uint64_t)x_mtiles * 64;  // 16-byte units per k-block of the activation
-  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)kb_lo * xkb + blockIdx.z * 128 + lane;
+  const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + (uint64_t)kb_lo * xkb + chunk * MT * 64 + lane;
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -82,7 +101,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
   // the launch coordinates only, so the summation order of an output does
   // not depend on the batch's row count.
   const uint32_t whole = chunks * UNROLL;
-  const uint32_t rot = whole ? ((blockIdx.x * WAVES + wave) * 7u + blockIdx.y * 5u) % whole : 0u;
+  const uint32_t rot = whole ? ((slice * WAVES + wave) * 7u + blockIdx.y * 5u) % whole : 0u;
   // Software pipeline over chunks of UNROLL k-blocks with two register sets:
   // the next chunk's loads are issued before the current chunk's MFMAs, and
   // scheduling barriers keep the compiler from sinking them back next to
@@ -194,20 +213,48 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
   }
 }
 
+// m <= 32: one chunk of 16 (MT = 1) or 32 (MT = 2) rows.
 template <int NT, int EPI, int WAVES, int UNROLL>
 void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                     const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
   const uint32_t kb = k / 32;
   const uint32_t kb_split = (kb + splits - 1) / splits;
-  const uint32_t chunks = (m + 31) / 32;
-  dim3 grid(n / (16 * NT), splits, chunks);
   const uint32_t x_mtiles = act_mtiles(m);
+  dim3 grid(n / (16 * NT), splits, 1);
   if (m <= 16)
     hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
                        x_mtiles, residual, out, ldo, err);
   else
     hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
                        x_mtiles, residual, out, ldo, err);
+}
+
+// 32 < m <= 256 (a speculative verify, a small prefill chunk): one split, the
+// rows in chunks of 64 (MT = 4, unroll 2) or 32 (MT = 2, unroll 4). The
+// 64-row chunk halves how often each weight tile is fetched; with 8 waves its
+// wave-partial buffer is 128 KiB of LDS (one workgroup per CU), so it is
+// taken there only when the launch fits in one round of the 256 CUs.
+// Measured at 160 rows (8B shapes, cold weights, us per launch):
+//   QKV 6144 x 4096    NT 4, 8 waves: 32-row 29.9, 64-row 38.1 (288 workgroups)
+//   O 4096 x 4096      NT 4, 8 waves: 32-row 28.3, 64-row 20.2
+//   down 4096 x 12288  NT 4, 8 waves: 32-row 78.5, 64-row 55.5
+//   gate/up 24576      64-row: NT 4 with 4 waves 94.2, NT 2 112.6 (32-row NT 2: 128.4)
+//   LM head 151936     NT 4, 4 waves: 32-row 788, 64-row 618
+template <int NT, int EPI, int WAVES>
+void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, const uint16_t* residual,
+                 void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  const uint32_t kb = k / 32;
+  const uint32_t x_mtiles = act_mtiles(m);
+  const uint32_t slices = n / (16 * NT);
+  if (WAVES == 8 && slices * ((m + 63) / 64) > 256) {
+    dim3 grid(slices, 1, (m + 31) / 32);
+    hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, 4>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb, x_mtiles,
+                       residual, out, ldo, err);
+  } else {
+    dim3 grid(slices, 1, (m + 63) / 64);
+    hipLaunchKernelGGL((gemm_kernel<NT, 4, EPI, WAVES, 2>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb, x_mtiles,
+                       residual, out, ldo, err);
+  }
 }
 
 // Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
@@ -219,6 +266,19 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  if constexpr (EPI != FH_EPI_PARTIAL) {
+    if (m > kMaxRows) {
+      if (n % 64 == 0 && n < 16384 && EPI != FH_EPI_SWIGLU)
+        launch_wide<4, EPI, 8>(xt, w, m, n, k, residual, out, ldo, err, s);
+      else if (n % 64 == 0)
+        launch_wide<4, EPI, 4>(xt, w, m, n, k, residual, out, ldo, err, s);
+      else if (n % 32 == 0)
+        launch_wide<2, EPI, 4>(xt, w, m, n, k, residual, out, ldo, err, s);
+      else if constexpr (EPI != FH_EPI_SWIGLU)
+        launch_wide<1, EPI, 4>(xt, w, m, n, k, residual, out, ldo, err, s);
+      return;
+    }
+  }
   if constexpr (EPI == FH_EPI_PARTIAL) {
     // Three n-tiles per wave where that puts exactly one workgroup on each
     // of the 256 CUs and four would leave some idle (the 8B QKV weight:

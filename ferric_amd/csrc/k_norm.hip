@@ -439,13 +439,19 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, uin
   return hipGetLastError();
 }
 
+// Row counts up to which the norms run one wave or workgroup per row (and
+// head) rather than the many-row kernels.
+constexpr uint32_t kWaveNormRows = 256;
+
 hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uint32_t splits, const uint16_t* q_norm,
                                  const uint16_t* k_norm, const float* cos_t, const float* sin_t,
                                  const uint32_t* positions, const uint32_t* table, uint16_t* q_out,
                                  uint16_t* k_cache, uint16_t* v_cache, uint32_t rows, uint32_t qh, uint32_t kvh,
                                  uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err,
                                  hipStream_t s) {
-  if (!qkv_part) {
+  // bf16 rows: up to 256 rows one wave per (row, head) as in decode (the
+  // 8B shape at 160 rows: 6400 waves); beyond that one lane per (row, head).
+  if (!qkv_part && rows > kWaveNormRows) {
     const uint64_t lanes = (uint64_t)rows * (qh + 2 * kvh);
     const QkvRopeArgs a{q_norm, k_norm, cos_t, sin_t, positions, table, q_out, k_cache, v_cache,
                         qh,     kvh,    stride, pages, context, eps,   err};
@@ -474,7 +480,9 @@ hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uin
 hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* w,
                                    uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float eps,
                                    uint32_t* err, hipStream_t s) {
-  if (!partials && y_tiled && rows > kMaxRows && width % 32 == 0 && width <= 4096) {
+  // One workgroup per row up to 256 rows (160 rows: 160 workgroups, where
+  // the 16-row-tile kernel would run 10), one per 16-row tile beyond.
+  if (!partials && y_tiled && rows > kWaveNormRows && width % 32 == 0 && width <= 4096) {
     hipLaunchKernelGGL(rmsnorm_tile_rows_kernel, dim3((rows + kTileRows - 1) / kTileRows), dim3(kTileThreads), 0, s,
                        hidden, w, y, rows, act_mtiles(rows), width, eps, err);
     return hipGetLastError();
