@@ -64,6 +64,7 @@ def build(verbose: bool = True) -> Path:
     if verbose:
         print(f"built {LIBRARY.relative_to(REPO_DIR)} from {len(sources)} sources", file=sys.stderr)
     build_c_host(verbose)
+    build_hip_checks(verbose)
     return LIBRARY
 
 
@@ -84,6 +85,25 @@ def build_c_host(verbose: bool = True) -> Path:
     if verbose:
         print(f"built {C_HOST_BIN.relative_to(REPO_DIR)}", file=sys.stderr)
     return C_HOST_BIN
+
+
+HIP_CHECKS = [REPO_DIR / "tests" / "hip" / "sqrt_rn_check.hip"]
+
+
+def build_hip_checks(verbose: bool = True) -> list:
+    """Compiles the standalone HIP check programs under tests/hip (each one
+    exercises a device helper directly; the GPU tests run them)."""
+    out = []
+    for src in HIP_CHECKS:
+        binary = src.with_suffix("")
+        cmd = [HIPCC, *[f for f in COMMON_FLAGS if f != "-fPIC"], "-o", str(binary), str(src)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+        if verbose:
+            print(f"built {binary.relative_to(REPO_DIR)}", file=sys.stderr)
+        out.append(binary)
+    return out
 
 
 if __name__ == "__main__":

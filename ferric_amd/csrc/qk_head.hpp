@@ -17,13 +17,36 @@ namespace fh {
 
 typedef unsigned int qk_u32x4 __attribute__((ext_vector_type(4)));
 
+// Correctly rounded square root of a positive normal float. The hardware
+// square root (v_sqrt_f32, what __fsqrt_rn becomes on this target) is only
+// within 1 ulp, so one correction step picks among its estimate s and the
+// neighbours s- and s+: the root rounds down to s- exactly when
+// x <= s- * s, and up to s+ exactly when x > s+ * s (both products exact
+// inside the FMA). A float x and either product differ by a multiple of
+// ulp(s)^2, while these thresholds sit within ulp(s)^2 / 4 of the true
+// rounding midpoints, so the comparisons decide exactly as the midpoints
+// would. Below 2^-64 those differences would underflow, so x is first
+// scaled by 2^64 and the root by 2^-32 (both exact). Checked against the
+// midpoint definition for every positive normal float.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const bool tiny = x < 0x1p-64f;
+  const float xs = tiny ? x * 0x1p64f : x;
+  const float s = __builtin_amdgcn_sqrtf(xs);
+  const uint32_t u = __builtin_bit_cast(uint32_t, s);
+  const float down = __builtin_bit_cast(float, u - 1u), up = __builtin_bit_cast(float, u + 1u);
+  float r = s;
+  if (__builtin_fmaf(-down, s, xs) <= 0.0f) r = down;
+  if (__builtin_fmaf(-up, s, xs) > 0.0f) r = up;
+  return tiny ? r * 0x1p-32f : r;
+}
+
 // Inverse RMS exactly as qwen3_rmsnorm_v1 forms it
 // (device/qwen3-all-kernels-v1/src/rmsnorm.rs:440-456): mean = sum / width
 // (a division), + epsilon, correctly rounded sqrt, then 1 / sqrt.
 __device__ __forceinline__ float inverse_rms(float sum, float width, float eps) {
-  float mean_square = sum / width;
+  float mean_square = __fdiv_rn(sum, width);
   float stabilized = mean_square + eps;
-  float denominator = __fsqrt_rn(stabilized);
+  float denominator = sqrt_rn(stabilized);
   return __fdiv_rn(1.0f, denominator);
 }
 
