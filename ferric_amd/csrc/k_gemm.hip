@@ -240,6 +240,8 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
 //   down 4096 x 12288  NT 4, 8 waves: 32-row 78.5, 64-row 55.5
 //   gate/up 24576      64-row: NT 4 with 4 waves 94.2, NT 2 112.6 (32-row NT 2: 128.4)
 //   LM head 151936     NT 4, 4 waves: 32-row 788, 64-row 618
+// Also slower on every shape: unroll 1, 2-wave workgroups, 128-row chunks
+// (gate/up 96 against 106-147, down 56 against 58-95).
 template <int NT, int EPI, int WAVES>
 void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, const uint16_t* residual,
                  void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
