@@ -5,8 +5,11 @@
 //
 // One step = 4 + 9 * layers kernel launches on one HIP stream, optionally
 // replayed from a HIP graph captured once per row count. All per-step inputs
-// (tokens, positions, page tables) live in one device block refreshed by a
-// single host-to-device copy, so a captured graph stays valid across steps.
+// (tokens, positions, page tables) live in one device block that the step's
+// first launch refreshes from a coherent pinned host block, and the last
+// launch stores the choices and error word into another, so a captured
+// graph stays valid across steps and a step needs no copy beside it.
+// Prefill chunks (run_prefill) keep a host-to-device copy of their metadata.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
