@@ -206,7 +206,23 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
   auto& wlds = *reinterpret_cast<u32x4(*)[WSTAGES][kBigTiles][64]>(lds_raw);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t bn = blockIdx.x * kBigTiles, bm = blockIdx.y * kBigTiles;
+  // Block order by XCD: workgroups go to the 8 XCDs round-robin in dispatch
+  // order, so with the plain order each XCD's co-resident workgroups cover
+  // 12 n-blocks x 3 m-blocks (8B gate/up) and its L2 holds that many weight
+  // and activation k-slices. Here XCD j takes m-blocks j, j + 8, ... four at
+  // a time and walks all n-blocks with them: its workgroups cover 4 m x 8 n
+  // blocks, fewer distinct operands per k-block (gate/up -4 %, O -8 %, QKV
+  // and down unchanged at 8192 rows; outputs identical). Grids whose m-block
+  // count is not a multiple of 32 keep the plain order.
+  uint32_t gx = blockIdx.x, gy = blockIdx.y;
+  if (gridDim.y % 32 == 0) {
+    const uint32_t NB = gridDim.x, b = blockIdx.x + NB * blockIdx.y;
+    const uint32_t r = b >> 3;  // position within this XCD's share
+    const uint32_t group = r / (4 * NB), within = r % (4 * NB);
+    gy = (group * 4 + within % 4) * 8 + (b & 7u);
+    gx = within / 4;
+  }
+  const uint32_t bn = gx * kBigTiles, bm = gy * kBigTiles;
   const int wn = wave % 2, wm = wave / 2;
   const uint32_t last = kb_count - 1;
   // The fused QKV epilogue's row lookups (position, page, slot) are
@@ -300,7 +316,7 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
     const uint32_t row = mt0 * 16 + lane;
     if (row < m)
       qknorm_rope_kv_head<32, true>(reinterpret_cast<const qk_u32x4*>(rows_lds + lane * kQkPitch), row,
-                              blockIdx.x * 2 + wn, qa, row_slot);
+                              gx * 2 + wn, qa, row_slot);
     return;
   }
   if (mt0 * 16 >= m) return;  // this wave's rows are all padding
