@@ -158,9 +158,10 @@ constexpr int kBigTiles = 16;  // 16-row tiles per block side (256 rows)
 // would wait for every load in flight, k-blocks ahead included.
 //
 // Counters on the gate/up projection (8192 x 24576 x 4096): 100.7M MFMAs of
-// 16 cycles keep the MFMA pipe busy 62 % of the kernel's cycles with no LDS
-// bank conflicts; the library GEMM reaches 85 % on the same shape but at a
-// lower clock under the board's power limit, about 10 % faster in time.
+// 16 cycles keep the MFMA pipe busy 66 % of the kernel's cycles (down 69 %,
+// O 58 %, fused QKV 56 %) with no LDS bank conflicts; the library GEMM
+// reaches 85 % on the gate/up shape but at a lower clock under the board's
+// power limit, about 10 % faster in time.
 constexpr unsigned xd_wait_vm(unsigned n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
 
 // Calls f(std::integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time.
