@@ -126,6 +126,7 @@ SIGNATURES = [
     ("fh_op_gemm", _st, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp, _vp]),
     ("fh_gemm_default_splits", _u32, [_u32, _u32]),
     ("fh_activation_rows", _u32, [_u32]),
+    ("fh_partial_slab_rows", _u32, [_u32]),
     ("fh_op_tile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_untile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_residual_rmsnorm", _st, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32, ctypes.c_float, _vp, _vp]),

@@ -1,5 +1,7 @@
 // K1 projections for decode (m <= 32 token rows): weight-streaming GEMM on
-// gfx950 MFMA (v_mfma_f32_16x16x32_bf16) with FP32 accumulation.
+// gfx950 MFMA (v_mfma_f32_16x16x32_bf16) with FP32 accumulation; for 33..256
+// rows the same weight stream against an activation panel shared through LDS
+// (gemm_panel_kernel below).
 //
 // Data layout. The weight W[n][k] is stored in MFMA tile order (common.hpp
 // tiled_offset) and the activation x[m][k] in activation tile order
@@ -13,7 +15,7 @@
 // contiguous range of k-blocks, and the WAVES waves of a workgroup split that
 // range again. Wave partials are added in wave order through LDS
 // (deterministic). Epilogues:
-//   FH_EPI_PARTIAL  FP32 partial sums, one [32][ldo] slab per split; the
+//   FH_EPI_PARTIAL  FP32 partial sums, one [partial_slab_rows(m)][ldo] slab per split; the
 //                    consumer adds the slabs in split order and rounds once
 //                    (residual + RMSNorm, QK-norm) — no atomics, no extra launch
 //   FH_EPI_BF16     out = bf16(acc)                       (gemm.rs:161 beta = 0)
@@ -26,6 +28,8 @@
 // gate and up narrowed before SwiGLU); the FP32 summation order is
 // reassociated (32-wide MFMA k-blocks, wave ranges, splits), as the
 // reference's own wave and MFMA profiles reassociate (v5 projection.rs:15, :241).
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "../../include/ferric_hip.h"
@@ -259,6 +263,205 @@ void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, 
   }
 }
 
+// 32 < m <= 256 rows, n % 128 == 0 (a speculative verify; the epilogues a
+// wide batch's projections use): the activation panel of each k-block is
+// staged in LDS once per workgroup and shared by its 4 waves; each wave
+// streams its own 2 weight tiles per k-block into a register ring. The
+// launches above read the activations once per 64 weight rows from L2 and
+// the weights once per row chunk; here each workgroup reads the activations
+// once per 128 weight rows and each weight tile once. Split-K across
+// workgroups (FH_EPI_PARTIAL) fills the CUs for the narrow projections; the
+// consumer adds the slabs in split order.
+//
+// MT: 16-row activation tiles computed (even, >= ceil(m / 16)). Per k-block
+// a wave issues its 2 weight tiles (register loads, LW = 4 k-blocks ahead)
+// and its share of the panel (XPW direct-to-LDS tile loads, LX k-blocks
+// ahead; the share is uniform, spare loads refetch tile MT - 1 into spare
+// slots). Direct-to-LDS loads and register loads complete out of order with
+// respect to each other (only loads of one kind complete in issue order), so
+// the wait before k-block kb is per kind: if W(kb) were outstanding, so
+// would be the 2 (LW - 1) weight loads after it; if the panel of kb were,
+// the XPW (LX - 1) panel loads after it. Waiting until at most the smaller
+// of the two counts is outstanding covers both. LX is sized per XPW so that
+// the weight count (6) is the smaller one and the weight stream keeps 3
+// k-blocks in flight; with a single count over both kinds (the loads of
+// one k-block assumed complete once all later ones were) the fast panel
+// loads overtook the weight stream and MFMAs read weight registers and
+// panel tiles before they arrived. Measured at 160 rows, cold weights, us
+// per launch (against the 64/32-row launches above): gate/up 24576 x 4096
+// 63 (95), down 4096 x 12288 in 8 splits 29 (56), O 4096 x 4096 in 8 splits
+// 14 (20), QKV 6144 x 4096 in 5 splits 19 (30), LM head 151936 x 4096 271
+// (617). 2 or 8 waves, 4 weight tiles per wave and 1 per wave were slower
+// on every shape.
+constexpr int kPanelWaves = 4, kPanelTilesPerWave = 2, kPanelLW = 4;
+static_assert(16 * kPanelWaves * kPanelTilesPerWave == kPanelCols, "a workgroup covers kPanelCols weight rows");
+constexpr int panel_xpw(int mt) { return (mt + kPanelWaves - 1) / kPanelWaves; }
+constexpr int panel_lx(int mt) {
+  return 1 + (kPanelTilesPerWave * (kPanelLW - 1) + panel_xpw(mt) - 1) / panel_xpw(mt);
+}
+
+constexpr unsigned panel_wait_vm(unsigned n) { return (n & 15u) | ((n >> 4) << 14) | (7u << 4) | (15u << 8); }
+
+template <int B, int E, class F>
+__device__ __forceinline__ void panel_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    panel_for<B + 1, E>(f);
+  }
+}
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(kPanelWaves * 64) void gemm_panel_kernel(const uint16_t* __restrict__ xt,
+                                                                     const uint16_t* __restrict__ w, uint32_t m,
+                                                                     uint32_t x_mtiles, uint32_t kb_count,
+                                                                     uint32_t kb_split, void* out, uint32_t ldo,
+                                                                     uint32_t* err) {
+  constexpr int WAVES = kPanelWaves, NTW = kPanelTilesPerWave, LW = kPanelLW, LX = panel_lx(MT);
+  constexpr int XPW = panel_xpw(MT), XT = XPW * WAVES, XST = LX + 1, WSL = LW + 1;
+  constexpr int P = LW > LX ? LW : LX;  // prologue steps
+  constexpr unsigned kWLater = NTW * (LW - 1), kXLater = XPW * (LX - 1);
+  constexpr unsigned kInFlight = kWLater < kXLater ? kWLater : kXLater;
+  static_assert(kInFlight < 64 && kInFlight >= kWLater, "the weight stream keeps LW - 1 k-blocks in flight");
+  __shared__ __attribute__((aligned(16))) u32x4 panel[XST][XT][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t slice = blockIdx.x, split = blockIdx.y;
+  const uint32_t kb_lo = split * kb_split;
+  // A split past the end of k (ceil rounding) writes zero partials.
+  const uint32_t nkb = kb_lo < kb_count ? min(kb_split, kb_count - kb_lo) : 0u;
+  const uint32_t tile0 = (slice * WAVES + wave) * NTW;
+
+  f32x4 acc[NTW][MT];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nkb > 0) {
+    const uint32_t last = nkb - 1;
+    // Workgroups start their k-range at staggered k-blocks (and wrap), so
+    // the grid's concurrent weight loads spread over the HBM channels. The
+    // order depends on the launch coordinates only, not on m.
+    const uint32_t rot = (slice * 7u + split * 5u) % nkb;
+    // k-block of step i; steps past the end repeat the last k-block, so the
+    // count of loads in flight is the same at every step.
+    auto kmap = [&](uint32_t i) -> uint64_t {
+      uint32_t j = min(i, last) + rot;
+      if (j >= nkb) j -= nkb;
+      return kb_lo + j;
+    };
+    const u32x4* wp = reinterpret_cast<const u32x4*>(w) + (uint64_t)tile0 * kb_count * 64 + lane;
+    const uint64_t w_tile = (uint64_t)kb_count * 64;
+    const u32x4* xp = reinterpret_cast<const u32x4*>(xt) + lane;
+    const uint64_t x_kb = (uint64_t)x_mtiles * 64;
+    u32x4 wr[WSL][NTW];
+    auto load_w = [&](auto slot_c, uint32_t i) {
+      const uint64_t k = kmap(i);
+#pragma unroll
+      for (int t = 0; t < NTW; ++t)
+        wr[decltype(slot_c)::value][t] = __builtin_nontemporal_load(wp + t * w_tile + k * 64);
+    };
+    auto fetch_x = [&](uint32_t i) {
+      const uint64_t k = kmap(i);
+      const uint32_t st = i % XST;
+#pragma unroll
+      for (int t = 0; t < XPW; ++t) {
+        const int j = wave + t * WAVES;
+        const int src = j < MT ? j : MT - 1;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(xp + k * x_kb + src * 64),
+                                         (__attribute__((address_space(3))) void*)&panel[st][j][0], 16, 0, 0);
+      }
+    };
+    // Prologue: W(0 .. LW - 1) and panels 0 .. LX - 1.
+    panel_for<0, P>([&](auto j_c) {
+      constexpr int j = decltype(j_c)::value - P;
+      if constexpr (j + LW >= 0) load_w(std::integral_constant<int, (j + LW) % WSL>{}, j + LW);
+      if constexpr (j + LX >= 0) fetch_x(j + LX);
+    });
+    auto step = [&](auto s_c, uint32_t kb) {
+      constexpr int S = decltype(s_c)::value;
+      __builtin_amdgcn_s_waitcnt(panel_wait_vm(kInFlight));
+      // Every wave's share of panel kb is in LDS, and every wave is done
+      // reading panel kb - 1, whose stage the next fetch overwrites.
+      __builtin_amdgcn_s_barrier();
+      load_w(std::integral_constant<int, (S + LW) % WSL>{}, kb + LW);
+      fetch_x(kb + LX);
+      const uint32_t st = kb % XST;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const u32x4 xv = panel[st][j][lane];
+#pragma unroll
+        for (int t = 0; t < NTW; ++t)
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(wr[S][t]), as_b8(xv), acc[t][j], 0, 0, 0);
+      }
+    };
+    uint32_t kb = 0;
+    for (; kb + WSL <= nkb; kb += WSL) panel_for<0, WSL>([&](auto s_c) { step(s_c, kb + decltype(s_c)::value); });
+    panel_for<0, WSL - 1>([&](auto s_c) {
+      if (kb + decltype(s_c)::value < nkb) step(s_c, kb + decltype(s_c)::value);
+    });
+    __builtin_amdgcn_s_waitcnt(panel_wait_vm(0));  // the repeated loads past the end
+  }
+
+  // D layout: lane l, element e holds weight row n = 16 nt + 4 (l / 16) + e
+  // and activation row m = 16 mt + l % 16.
+  const uint32_t q = lane >> 4, c = lane & 15;
+  if constexpr (EPI == FH_EPI_SWIGLU) {
+    bool bad = false;
+#pragma unroll
+    for (int p = 0; p < NTW / 2; ++p) {
+      const uint32_t col = ((tile0 + 2 * p) / 2) * 16 + 4 * q;  // first of 4 output columns
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const uint32_t row = j * 16 + c;
+        if (row >= m) continue;
+        uint32_t y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = swiglu_bf16(round_bf16(acc[2 * p][j][e]), round_bf16(acc[2 * p + 1][j][e]), bad);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + act_offset_m(row, col, act_mtiles(m))) =
+            make_uint2(y[0] | (y[1] << 16), y[2] | (y[3] << 16));
+      }
+    }
+    if (bad) raise_error(err, ERR_NONFINITE);
+  } else {
+    static_assert(EPI == FH_EPI_PARTIAL || EPI == FH_EPI_F32, "panel epilogues");
+    float* o = reinterpret_cast<float*>(out) + (EPI == FH_EPI_PARTIAL ? (uint64_t)split * kPanelRows * ldo : 0u);
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      const uint32_t n = (tile0 + t) * 16 + 4 * q;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const uint32_t row = j * 16 + c;
+        if (row < m) *reinterpret_cast<f32x4*>(o + (uint64_t)row * ldo + n) = acc[t][j];
+      }
+    }
+  }
+}
+
+template <int EPI>
+void launch_panel(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
+                  void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  const uint32_t kb = k / 32;
+  const uint32_t kb_split = (kb + splits - 1) / splits;
+  const dim3 grid(n / kPanelCols, splits);
+  uint32_t mt = (m + 15) / 16;
+  mt += mt & 1u;
+#define FH_PANEL(MT_)                                                                                        \
+  hipLaunchKernelGGL((gemm_panel_kernel<MT_, EPI>), grid, dim3(kPanelWaves * 64), 0, s, xt, w, m, act_mtiles(m), \
+                     kb, kb_split, out, ldo, err)
+  switch (mt) {
+    case 4: FH_PANEL(4); break;
+    case 6: FH_PANEL(6); break;
+    case 8: FH_PANEL(8); break;
+    case 10: FH_PANEL(10); break;
+    case 12: FH_PANEL(12); break;
+    case 14: FH_PANEL(14); break;
+    default: FH_PANEL(16); break;
+  }
+#undef FH_PANEL
+}
+
 // Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
 // cold weights): weights of up to 16K rows use NT = 4 (activation traffic
 // half the weight traffic) with 8 waves, or NT = 3 for split-K partials when
@@ -268,6 +471,12 @@ void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, 
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  if constexpr (EPI == FH_EPI_PARTIAL || EPI == FH_EPI_SWIGLU || EPI == FH_EPI_F32) {
+    if (m > kMaxRows && m <= kPanelRows && n % kPanelCols == 0) {
+      launch_panel<EPI>(xt, w, m, n, k, splits, out, ldo, err, s);
+      return;
+    }
+  }
   if constexpr (EPI != FH_EPI_PARTIAL) {
     if (m > kMaxRows) {
       if (n % 64 == 0 && n < 16384 && EPI != FH_EPI_SWIGLU)
@@ -317,10 +526,22 @@ uint32_t choose_splits(uint32_t n, uint32_t k) {
 
 uint32_t gemm_default_splits(uint32_t n, uint32_t k) { return choose_splits(n, k); }
 
+// 33..256 rows: about 256 workgroups of 128 weight rows, each split keeping
+// at least 16 k-blocks (8B shapes: QKV 5, O 8, down 8, gate/up 1).
+uint32_t gemm_panel_splits(uint32_t n, uint32_t k) {
+  const uint32_t slices = n / kPanelCols, kb = k / 32;
+  uint32_t s = slices ? 256 / slices : 1;
+  const uint32_t max_s = kb / 16 > 0 ? kb / 16 : 1;
+  if (s > max_s) s = max_s;
+  return s < 1 ? 1 : s;
+}
+
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        uint32_t* err, hipStream_t s) {
-  if (splits == 0 || (m > kMaxRows && (splits != 1 || epilogue == FH_EPI_PARTIAL))) return hipErrorInvalidValue;
+  if (splits == 0) return hipErrorInvalidValue;
+  if (m > kMaxRows && (epilogue == FH_EPI_PARTIAL ? !gemm_partial_rows_ok(m, n) : splits != 1))
+    return hipErrorInvalidValue;
   switch (epilogue) {
     case FH_EPI_BF16: launch_epi<FH_EPI_BF16>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;
     case FH_EPI_RESIDUAL: launch_epi<FH_EPI_RESIDUAL>(x_tiled, w_tiled, m, n, k, 1, residual, out, ldo, err, s); break;

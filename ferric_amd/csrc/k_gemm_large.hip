@@ -198,8 +198,14 @@ __global__ __launch_bounds__(512) void gemm_large_xd_kernel(const uint16_t* __re
                                                             uint32_t* err) {
   static_assert(LX >= 1 && LW >= LX, "weights requested no later than activations");
   constexpr int WN = 8, WM = 4, WSTAGES = LW + 1, XSLOTS = LX + 1;
-  // Loads issued after X(kb): 2 weight and WM activation loads per later k-block.
-  constexpr unsigned kInFlight = (2 + WM) * (LX - 1);
+  // The wait before k-block kb counts per kind: direct-to-LDS loads (the
+  // weight tiles) and register loads (the activation tiles) complete out of
+  // order with respect to each other, only loads of one kind in issue order.
+  // If W(kb) were outstanding, so would be the 2 (LW - 1) weight loads after
+  // it; if X(kb) were, the WM (LX - 1) activation loads after it. At most the
+  // smaller count outstanding covers both.
+  constexpr unsigned kWLater = 2 * (LW - 1), kXLater = WM * (LX - 1);
+  constexpr unsigned kInFlight = kWLater < kXLater ? kWLater : kXLater;
   static_assert(kInFlight < 64, "vmcnt range");
   constexpr size_t kRingBytes = sizeof(u32x4) * WSTAGES * kBigTiles * 64;
   constexpr size_t kStageBytes = EPI == kEpiQkvRope ? 4ull * 8 * 64 * kQkPitch : 0;

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kHeadsPerGroup * 64) void qknorm_rope_kv_kernel(
     const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint32_t qh,
-    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t* err) {
+    uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context, float eps, uint32_t slab_rows, uint32_t* err) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t head = blockIdx.x * kHeadsPerGroup + (threadIdx.x >> 6);
   const uint32_t row = blockIdx.y;
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kHeadsPerGroup * 64) void qknorm_rope_kv_kernel(
     a = bf16_to_f32(qkv[base]);
     b = bf16_to_f32(qkv[base + 64]);
   } else {
-    const uint64_t slab = (uint64_t)kMaxRows * ld;
+    const uint64_t slab = (uint64_t)slab_rows * ld;
     if constexpr (S > 0) {
       float pa[S], pb[S];
 #pragma unroll
@@ -206,13 +206,14 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
                                                                         uint32_t splits,
                                                                         const uint16_t* __restrict__ w,
                                                                         uint16_t* __restrict__ y, uint32_t y_mtiles,
-                                                                        uint32_t width, float eps, uint32_t* err) {
+                                                                        uint32_t width, float eps, uint32_t slab_rows,
+                                                                        uint32_t* err) {
   __shared__ float red[kNormThreads / 64];
   const uint32_t row = blockIdx.x;
   uint16_t* hr = hidden + (uint64_t)row * width;
   const uint32_t chunks = width / 8;
   constexpr int kMaxPerThread = 4;  // width <= 8192
-  const uint64_t slab = (uint64_t)kMaxRows * width;
+  const uint64_t slab = (uint64_t)slab_rows * width;
   uint4 v[kMaxPerThread], wv[kMaxPerThread];
   float sum = 0.f;
   bool bad = false;
@@ -462,13 +463,15 @@ hipError_t launch_qknorm_rope_kv(const uint16_t* qkv, const float* qkv_part, uin
   const dim3 block(kHeadsPerGroup * 64);
 #define FH_QKNORM(S_)                                                                                              \
   hipLaunchKernelGGL(qknorm_rope_kv_kernel<S_>, grid, block, 0, s, qkv, qkv_part, splits, q_norm, k_norm, cos_t,  \
-                     sin_t, positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context, eps, err)
+                     sin_t, positions, table, q_out, k_cache, v_cache, qh, kvh, stride, pages, context, eps,           \
+                     partial_slab_rows(rows), err)
   switch (qkv_part ? splits : 0) {
     case 0: FH_QKNORM(0); break;
     case 1: FH_QKNORM(1); break;
     case 2: FH_QKNORM(2); break;
     case 3: FH_QKNORM(3); break;
     case 4: FH_QKNORM(4); break;
+    case 5: FH_QKNORM(5); break;
     case 6: FH_QKNORM(6); break;
     case 8: FH_QKNORM(8); break;
     default: FH_QKNORM(-1); break;
@@ -489,7 +492,7 @@ hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint
   }
 #define FH_RESNORM(S_)                                                                                             \
   hipLaunchKernelGGL(residual_rmsnorm_kernel<S_>, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, \
-                     y, y_tiled ? act_mtiles(rows) : 0u, width, eps, err)
+                     y, y_tiled ? act_mtiles(rows) : 0u, width, eps, partial_slab_rows(rows), err)
   switch (partials ? splits : 0) {
     case 0: FH_RESNORM(0); break;
     case 1: FH_RESNORM(1); break;

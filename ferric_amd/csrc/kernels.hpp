@@ -37,6 +37,17 @@ constexpr uint32_t kLargeBlockRows = 256;
 __host__ __device__ inline uint32_t act_mtiles(uint32_t m) {
   return m <= kMaxRows ? 2u : ((m + kLargeBlockRows - 1) / kLargeBlockRows) * (kLargeBlockRows / 16);
 }
+// Batches of kMaxRows < m <= kPanelRows rows (a speculative verify) run the
+// panel GEMM over slices of kPanelCols weight rows, which also writes split-K
+// partials. A split-K partial slab holds partial_slab_rows(m) rows: 32 for
+// decode batches, 256 for these.
+constexpr uint32_t kPanelRows = 256;
+constexpr uint32_t kPanelCols = 128;
+__host__ __device__ inline uint32_t partial_slab_rows(uint32_t m) { return m <= kMaxRows ? kMaxRows : kPanelRows; }
+// Whether FH_EPI_PARTIAL is supported at m rows and n output columns.
+inline bool gemm_partial_rows_ok(uint32_t m, uint32_t n) {
+  return m <= kMaxRows || (m <= kPanelRows && n % kPanelCols == 0);
+}
 
 inline uint32_t attn_max_splits(uint32_t context_tokens, uint32_t split_pages) {
   return (context_tokens + split_pages * 16 - 1) / (split_pages * 16);
@@ -109,6 +120,8 @@ hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        uint32_t* err, hipStream_t s);
 uint32_t gemm_default_splits(uint32_t n, uint32_t k);
+// Split-K factor for kMaxRows < m <= kPanelRows (n % kPanelCols == 0).
+uint32_t gemm_panel_splits(uint32_t n, uint32_t k);
 
 // attention
 // out: [rows][qh*128] row-major, or activation tile order when out_tiled.

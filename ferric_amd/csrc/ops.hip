@@ -74,9 +74,14 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
     return FH_ERR_INVALID_ARGUMENT;
   }
   if (m > fh::kMaxRows) {
-    // Prefill-size batches: 128 x 128 blocks, no split-K, 8-byte aligned rows.
-    if (epilogue == FH_EPI_PARTIAL || n % (16 * 8) || (epilogue != FH_EPI_SWIGLU && ldo % 4))
-      return FH_ERR_INVALID_ARGUMENT;
+    // Wide and prefill-size batches: n % 128 == 0, 16-byte aligned FP32 rows
+    // (8-byte bf16 rows); split-K partials up to kPanelRows rows.
+    if (n % fh::kPanelCols || (epilogue != FH_EPI_SWIGLU && ldo % 4)) return FH_ERR_INVALID_ARGUMENT;
+    if (epilogue == FH_EPI_PARTIAL) {
+      if (!fh::gemm_partial_rows_ok(m, n)) return FH_ERR_INVALID_ARGUMENT;
+      return from_hip(fh::launch_gemm(x_tiled, w_tiled, m, n, k, epilogue, splits, residual, out, ldo, error_word,
+                                      as_stream(stream)));
+    }
     return from_hip(fh::launch_gemm_large(x_tiled, w_tiled, m, n, k, epilogue, residual, out, ldo, error_word,
                                                   as_stream(stream)));
   }
@@ -87,6 +92,8 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
 uint32_t fh_activation_rows(uint32_t m) { return m ? fh::act_mtiles(m) * 16 : 0u; }
 
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k) { return fh::gemm_default_splits(n, k); }
+
+uint32_t fh_partial_slab_rows(uint32_t m) { return m == 0 || m > fh::kPanelRows ? 0u : fh::partial_slab_rows(m); }
 
 fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream) {
   if (!x || !x_tiled || m == 0 || k == 0 || k % 32) return FH_ERR_INVALID_ARGUMENT;
@@ -103,7 +110,7 @@ fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32
                                  uint32_t* error_word, void* stream) {
   if (!hidden || !weight || !y || rows == 0 || width == 0 || width % 32 || width > 8192 || (splits && !partials))
     return FH_ERR_INVALID_ARGUMENT;
-  if (splits && rows > fh::kMaxRows) return FH_ERR_INVALID_ARGUMENT;
+  if (splits && rows > fh::kPanelRows) return FH_ERR_INVALID_ARGUMENT;
   return from_hip(fh::launch_residual_rmsnorm(hidden, partials, splits, weight, y, y_tiled, rows, width, epsilon,
                                               error_word, as_stream(stream)));
 }
@@ -116,7 +123,7 @@ fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint1
                                void* stream) {
   if (!qkv || !q_norm || !k_norm || !cos_table || !sin_table || !positions || !page_table || !q_out || !k_cache ||
       !v_cache || rows == 0 || query_heads == 0 || kv_heads == 0 || query_heads + 2 * kv_heads > 64 || stride == 0 ||
-      physical_pages == 0 || context_tokens == 0 || (qkv_splits && rows > fh::kMaxRows))
+      physical_pages == 0 || context_tokens == 0 || (qkv_splits && rows > fh::kPanelRows))
     return FH_ERR_INVALID_ARGUMENT;
   const uint16_t* bf = qkv_splits ? nullptr : reinterpret_cast<const uint16_t*>(qkv);
   const float* part = qkv_splits ? reinterpret_cast<const float*>(qkv) : nullptr;

@@ -105,6 +105,11 @@ struct fh_ctx {
     uint16_t* act = nullptr;       // tiled
     uint16_t* out_hidden = nullptr;  // gathered output rows [kMaxPrefillOutputs][hidden]
     uint16_t* out_xn = nullptr;    // tiled
+    // Split-K partial slabs of chunks of up to kPanelRows rows, shared by the
+    // QKV, O and down projections of a layer (each consumed before the next
+    // is written): [splits][partial_slab_rows(rows)][n].
+    float* part = nullptr;
+    uint32_t s_qkv = 1, s_o = 1, s_down = 1;  // splits for kMaxRows < rows <= kPanelRows
     float* logits = nullptr;       // [kMaxPrefillOutputs][vocab]
     void* argmax_scratch = nullptr;
     uint32_t* choices = nullptr;
@@ -623,6 +628,14 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
     TRY(dalloc(ctx, &p.act, tiled_rows * I));
     TRY(dalloc(ctx, &p.out_hidden, (uint64_t)kMaxPrefillOutputs * H));
     TRY(dalloc(ctx, &p.out_xn, out_tiled_rows * H));
+    p.s_qkv = fh::gemm_panel_splits(ctx->nqkv, H);
+    p.s_o = fh::gemm_panel_splits(H, Q);
+    p.s_down = fh::gemm_panel_splits(H, I);
+    const uint64_t part_floats =
+        std::max({(uint64_t)p.s_qkv * fh::kPanelRows * ctx->nqkv, (uint64_t)p.s_o * fh::kPanelRows * H,
+                  (uint64_t)p.s_down * fh::kPanelRows * H, (uint64_t)ctx->s_qkv * kMaxRows * ctx->nqkv,
+                  (uint64_t)ctx->s_o * kMaxRows * H, (uint64_t)ctx->s_down * kMaxRows * H});
+    TRY(dalloc(ctx, &p.part, part_floats));
     TRY(dalloc(ctx, &p.logits, (uint64_t)kMaxPrefillOutputs * V));
     TRY(dalloc(ctx, reinterpret_cast<uint8_t**>(&p.argmax_scratch), fh_argmax_scratch_bytes(kMaxPrefillOutputs)));
     TRY(dalloc(ctx, &p.choices, kMaxPrefillOutputs));
@@ -850,8 +863,11 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
 }
 
 // A prefill chunk (row_capacity < nrows <= prefill_rows), launched eagerly:
-// the decode path's op order (batched.rs:1746-2454) with the compute-bound
-// projections, bf16 QKV rows into the QK-norm kernel, attention over blocks
+// the decode path's op order (batched.rs:1746-2454). Up to 256 rows (a
+// speculative verify) the projections are the panel GEMM with split-K
+// partials folded by the norms, as in a decode step; beyond that the
+// compute-bound 256 x 256-block kernel with the residual (and, for QKV, the
+// QK-norm, RoPE and KV append) in its epilogues. Attention runs over blocks
 // of consecutive rows of one sequence (each K/V page read once per block),
 // and the final norm + FP32 head + argmax over the requested output rows
 // only.
@@ -916,15 +932,24 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   const uint32_t R = nrows;
   // The fused QKV epilogue needs the 256 x 256-block projection kernel.
   const bool fused_qkv = R > 256 && ctx->nqkv % 256 == 0 && fh::act_mtiles(R) % 16 == 0;
+  // Chunks of up to kPanelRows rows (a speculative verify) write split-K
+  // partials for QKV, O and down: the QK-norm, the post-attention norm and
+  // the next layer's input norm (after the last layer the final norm, whose
+  // output is unused here) fold them, as in a decode step. Larger chunks
+  // keep the residual in the projection epilogues.
+  const bool split_k = R <= fh::kPanelRows;
+  const uint32_t sq = R <= kMaxRows ? ctx->s_qkv : p.s_qkv, so = R <= kMaxRows ? ctx->s_o : p.s_o,
+                 sd = R <= kMaxRows ? ctx->s_down : p.s_down;
   L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, p.hidden, R, H, V, err, s); });
   for (uint32_t l = 0; l < md.layers; ++l) {
     const LayerWeights& W = ctx->layers[l];
     uint16_t* kc = kv_cache(ctx, l, 0);
     uint16_t* vc = kv_cache(ctx, l, 1);
-    L(FH_KC_RMSNORM, [&] {
-      return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.in_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
-    });
+    if (!split_k || l == 0)
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.in_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
+      });
     if (fused_qkv) {
       // QK-norm, RoPE and the KV append run in the projection's epilogue.
       const fh::QkvRopeArgs qa{W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, p.qrot, kc, vc,
@@ -932,29 +957,54 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
       L(FH_KC_QKV_GEMM, [&] { return fh::launch_gemm_qkv_rope(p.xn, W.qkv, R, ctx->nqkv, H, qa, s); });
     } else {
       L(FH_KC_QKV_GEMM, [&] {
-        return fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv, ctx->nqkv, err, s);
+        return split_k ? fh::launch_gemm(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, p.part,
+                                         ctx->nqkv, err, s)
+                       : fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv,
+                                               ctx->nqkv, err, s);
       });
       L(FH_KC_QKNORM_ROPE_KV, [&] {
-        return fh::launch_qknorm_rope_kv(p.qkv, nullptr, 0, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab,
-                                         p.qrot, kc, vc, R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
+        return fh::launch_qknorm_rope_kv(split_k ? nullptr : p.qkv, split_k ? p.part : nullptr, split_k ? sq : 0,
+                                         W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, p.qrot, kc, vc,
+                                         R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
       });
     }
     L(FH_KC_ATTENTION, [&] {
       return fh::launch_attention_blocks(p.qrot, kc, vc, d_pos, d_tab, d_blocks, nblocks, p.attn, 1, R, QH, KVH,
                                          stride, pages, C, err, s);
     });
-    L(FH_KC_O_GEMM, [&] {
-      return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
-    });
-    L(FH_KC_RMSNORM, [&] {
-      return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.post_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
-    });
+    if (split_k) {
+      L(FH_KC_O_GEMM, [&] {
+        return fh::launch_gemm(p.attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, p.part, H, err, s);
+      });
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(p.hidden, p.part, so, W.post_norm, p.xn, 1, R, H, md.rms_epsilon, err,
+                                           s);
+      });
+    } else {
+      L(FH_KC_O_GEMM, [&] {
+        return fh::launch_gemm_large(p.attn, W.o, R, H, Q, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
+      });
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(p.hidden, nullptr, 0, W.post_norm, p.xn, 1, R, H, md.rms_epsilon, err,
+                                           s);
+      });
+    }
     L(FH_KC_GATE_UP_GEMM, [&] {
       return fh::launch_gemm_large(p.xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, nullptr, p.act, I, err, s);
     });
-    L(FH_KC_DOWN_GEMM, [&] {
-      return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
-    });
+    if (split_k) {
+      const uint16_t* next_norm = l + 1 < md.layers ? ctx->layers[l + 1].in_norm : ctx->final_norm;
+      L(FH_KC_DOWN_GEMM, [&] {
+        return fh::launch_gemm(p.act, W.down, R, H, I, FH_EPI_PARTIAL, sd, nullptr, p.part, H, err, s);
+      });
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(p.hidden, p.part, sd, next_norm, p.xn, 1, R, H, md.rms_epsilon, err, s);
+      });
+    } else {
+      L(FH_KC_DOWN_GEMM, [&] {
+        return fh::launch_gemm_large(p.act, W.down, R, H, I, FH_EPI_RESIDUAL, p.hidden, p.hidden, H, err, s);
+      });
+    }
     if (ctx->capture)
       L(FH_KC_RMSNORM, [&] {
         return fh::launch_copy_u16(p.hidden, ctx->capture + (uint64_t)l * ctx->capture_rows * H, (uint64_t)R * H, s);

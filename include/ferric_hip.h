@@ -222,16 +222,20 @@ fh_status fh_op_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y, 
  * epilogue: FH_EPI_BF16 (one RNE), FH_EPI_RESIDUAL (bf16((0 + acc) + residual), may alias out),
  * FH_EPI_SWIGLU (w from fh_op_tile_gate_up, n = 2*i, out [m][i] = swiglu(bf16(g), bf16(u))),
  * FH_EPI_F32 (FP32 out, the LM head). m <= 32 streams the weight (decode, split-K allowed);
- * m > 32 runs the compute-bound prefill kernel (256 x 256 blocks through LDS when
- * n % 256 == 0, else 128 x 128 blocks; n % 128 == 0, splits = 1, ldo % 4 == 0,
- * no FH_EPI_PARTIAL). Replaces gemm.rs:161/:605 and
+ * m > 32 needs n % 128 == 0 and ldo % 4 == 0: up to 256 rows FH_EPI_PARTIAL, FH_EPI_SWIGLU
+ * and FH_EPI_F32 run the panel kernel (activation panel shared through LDS; split-K allowed
+ * for FH_EPI_PARTIAL), the other epilogues the weight-streaming kernel over row chunks
+ * (splits = 1); beyond 256 rows the compute-bound prefill kernel (256 x 256 blocks through
+ * LDS when n % 256 == 0, else 128 x 128 blocks; splits = 1, no FH_EPI_PARTIAL). Replaces
+ * gemm.rs:161/:605 and
  * device/qwen3-tp-batch32-kernels-v5/src/projection.rs:15/:142/:241, collective.rs:25,
  * activation.rs:32 and device/qwen3-tp-fp32-head32-kernels-v8/src/projection.rs:66/:186. */
 enum { FH_EPI_BF16 = 0, FH_EPI_RESIDUAL = 1, FH_EPI_SWIGLU = 2, FH_EPI_F32 = 3, FH_EPI_PARTIAL = 4 };
 /* x_tiled is in activation tile order (fh_op_tile_activation). FH_EPI_SWIGLU writes its
  * output in activation tile order (the down projection's input); FH_EPI_PARTIAL writes
- * FP32 partial sums as `splits` slabs of [32][ldo] (split-K across workgroups; the
- * consumer adds the slabs in order and rounds once). Other epilogues use splits = 1.
+ * FP32 partial sums as `splits` slabs of [fh_partial_slab_rows(m)][ldo] (split-K across
+ * workgroups; the consumer adds the slabs in order and rounds once; a split past the end
+ * of k writes zeros). Other epilogues use splits = 1.
  * error_word (may be NULL) receives the nonfinite bit where the SwiGLU epilogue meets a
  * nonfinite gate, up or product (qwen3_swiglu_bf16_f32_v1 traps there). */
 fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
@@ -241,6 +245,10 @@ fh_status fh_op_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t 
 uint32_t fh_gemm_default_splits(uint32_t n, uint32_t k);
 /* Rows a tiled activation buffer for m rows holds: 32 for m <= 32, else m rounded up to 256. */
 uint32_t fh_activation_rows(uint32_t m);
+/* Rows of one FH_EPI_PARTIAL slab for an m-row batch: 32 for m <= 32, 256 for 32 < m <= 256,
+ * 0 (no split-K partials) otherwise. No counterpart in the reference, whose split-K
+ * partials are per-step buffers of its decode path (v5 collective.rs:25-60). */
+uint32_t fh_partial_slab_rows(uint32_t m);
 /* Row-major [m][k] bf16 <-> activation tile order (the tiled buffer holds fh_activation_rows(m) x k). */
 fh_status fh_op_tile_activation(const uint16_t* x, uint16_t* x_tiled, uint32_t m, uint32_t k, void* stream);
 fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t m, uint32_t k, void* stream);
@@ -249,15 +257,15 @@ fh_status fh_op_untile_activation(const uint16_t* x_tiled, uint16_t* x, uint32_t
  * hidden[r]) is written back first (the TP1 residual, v5 collective.rs:25-60, with the split-K
  * slabs summed in order), then y = RMSNorm(hidden) is written in activation tile order
  * (y_tiled = 1, fh_activation_rows(rows) rows) or row-major. partials: `splits` slabs of
- * [32][width] FP32 (rows <= 32 when splits > 0). */
+ * [fh_partial_slab_rows(rows)][width] FP32 (rows <= 256 when splits > 0). */
 fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32_t splits, const uint16_t* weight,
                                  uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float epsilon,
                                  uint32_t* error_word, void* stream);
 
 /* K3 per-head QK-norm + split-half RoPE + paged KV append, one launch.
  * qkv: [rows][(qh + 2*kvh) * 128] bf16 projection output when qkv_splits == 0, else
- * qkv_splits FP32 partial slabs of [32][(qh + 2*kvh) * 128] (each value = bf16 of the ordered
- * slab sum); q_out: [rows][qh*128] rotated queries;
+ * qkv_splits FP32 partial slabs of [fh_partial_slab_rows(rows)][(qh + 2*kvh) * 128] (rows <= 256;
+ * each value = bf16 of the ordered slab sum); q_out: [rows][qh*128] rotated queries;
  * k_cache/v_cache: [pages][16][kvh][128]; cos/sin: [context][64] f32 table;
  * page_table: [rows][stride]. Replaces qwen3_rmsnorm_v1 at width 128 (batched.rs:1956-1982),
  * qwen3_rope_v1 (rope_kv.rs:102) and qwen3_paged_kv_write_v1 (rope_kv.rs:261). */

@@ -99,7 +99,8 @@ def test_ops_reject_bad_shapes_before_any_launch():
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     assert lib.fh_op_gemm(p, p, 0, 64, 64, 0, 1, None, p, 64, None, None) == 1  # m = 0
     assert lib.fh_op_gemm(p, p, 33, 64, 64, 0, 1, None, p, 64, None, None) == 1  # m > 32 needs n % 128
-    assert lib.fh_op_gemm(p, p, 33, 128, 64, 4, 1, None, p, 128, None, None) == 1  # m > 32: no split-K partials
+    assert lib.fh_op_gemm(p, p, 257, 128, 64, 4, 1, None, p, 128, None, None) == 1  # partials above 256 rows
+    assert lib.fh_op_gemm(p, p, 33, 128, 64, 4, 1, None, p, 130, None, None) == 1  # partials: 16-byte aligned rows
     assert lib.fh_op_gemm(p, p, 33, 128, 64, 0, 1, None, p, 130, None, None) == 1  # m > 32: 8-byte aligned rows
     assert lib.fh_op_gemm(p, p, 4, 60, 64, 0, 1, None, p, 64, None, None) == 1  # n % 16
     assert lib.fh_op_gemm(p, p, 4, 64, 48, 0, 1, None, p, 64, None, None) == 1  # k % 32
@@ -111,10 +112,13 @@ def test_ops_reject_bad_shapes_before_any_launch():
     assert lib.fh_op_tile_activation(p, p, 33, 48, None) == 1  # k % 32
     assert lib.fh_activation_rows(1) == 32 and lib.fh_activation_rows(32) == 32
     assert lib.fh_activation_rows(33) == 256 and lib.fh_activation_rows(257) == 512
+    # split-K partial slabs: 32 rows for decode batches, 256 for wide ones, none beyond
+    assert [lib.fh_partial_slab_rows(m) for m in (0, 1, 32, 33, 256, 257)] == [0, 32, 32, 256, 256, 0]
     ms = ctypes.c_float()
     assert lib.fh_time_attention(None, 1, ctypes.byref(ms)) == 1  # no context
     assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1
     assert lib.fh_op_residual_rmsnorm(p, None, 2, p, p, 1, 4, 4096, 1e-6, None, None) == 1  # partials missing
+    assert lib.fh_op_residual_rmsnorm(p, p, 2, p, p, 1, 257, 4096, 1e-6, None, None) == 1  # partials above 256 rows
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
 

@@ -187,9 +187,10 @@ def _gemm_case(m, n, k, epi, seed, splits=1, poison_row=None):
         return got, orc.swiglu(g, u)
     _lib.check(LIB.fh_op_tile_weight(du.ptr(dw_), du.ptr(dt), n, k, du.stream()))
     if epi == _lib.EPI_PARTIAL:
-        out = du.empty(splits * 32 * n, np.float32)
+        slab_rows = int(LIB.fh_partial_slab_rows(m))
+        out = du.to_dev(np.full(splits * slab_rows * n, np.nan, np.float32))  # every slab row < m is written
         _lib.check(LIB.fh_op_gemm(du.ptr(dxt), du.ptr(dt), m, n, k, epi, splits, None, du.ptr(out), n, None, du.stream()))
-        slabs = du.to_host(out, np.float32).reshape(splits, 32, n)[:, :m]
+        slabs = du.to_host(out, np.float32).reshape(splits, slab_rows, n)[:, :m]
         total = slabs[0].copy()
         for sp in range(1, splits):
             total = (total + slabs[sp]).astype(np.float32)
@@ -230,6 +231,17 @@ def test_gemm_split_k_partials(m, n, k, splits):
     assert np.max(np.abs(got - ref)) <= F32_BOUND
 
 
+# 33-256 rows: the panel kernel, one instance per even m-tile count (4 .. 16
+# tiles), slabs of 256 rows; (48, 128, 256, 5): 8 k-blocks in splits of 2, so
+# the fifth split is past the end of k and must write zeros.
+@pytest.mark.parametrize("m,n,k,splits", [(33, 128, 1024, 2), (80, 384, 2048, 3), (100, 6144, 1024, 5),
+                                          (160, 1024, 4096, 8), (176, 256, 4096, 4), (200, 256, 2048, 3),
+                                          (256, 128, 1024, 4), (48, 128, 256, 5), (130, 512, 512, 1)])
+def test_gemm_wide_split_k_partials(m, n, k, splits):
+    got, ref = _gemm_case(m, n, k, _lib.EPI_PARTIAL, 37 * m + splits + n, splits=splits)
+    assert np.max(np.abs(got - ref)) <= F32_BOUND
+
+
 @pytest.mark.parametrize("m", [3, 32])
 def test_gemm_residual_and_swiglu_epilogues(m):
     got, ref = _gemm_case(m, 512, 4096, _lib.EPI_RESIDUAL, 99 + m)
@@ -255,8 +267,9 @@ def test_gemm_swiglu_epilogue_reports_nonfinite(m):
 @pytest.mark.parametrize("m", [33, 130, 257])
 @pytest.mark.parametrize("n,k", [(128, 64), (256, 1024), (384, 4096)])
 def test_gemm_large_m_bf16_and_f32_epilogues(m, n, k):
-    # 33-256 rows: the decode kernel over row chunks; 257 rows: the
-    # compute-bound kernel (128 x 128 blocks, no split-K).
+    # 33-256 rows: the panel kernel (FP32) and the decode kernel over row
+    # chunks (bf16); 257 rows: the compute-bound kernel (128 x 128 blocks,
+    # no split-K).
     got, ref = _gemm_case(m, n, k, _lib.EPI_F32, m * 5 + n)
     assert np.max(np.abs(got - ref)) <= F32_BOUND
     got, ref = _gemm_case(m, n, k, _lib.EPI_BF16, m * 5 + n + 1)
@@ -267,10 +280,10 @@ def test_gemm_large_m_bf16_and_f32_epilogues(m, n, k):
 @pytest.mark.parametrize("m,n,k,epi", [(160, 6144, 1024, "bf16"), (160, 6144, 1024, "f32"), (100, 24576, 256, "swiglu"),
                                        (70, 4096, 2048, "residual")])
 def test_gemm_wide_batches(m, n, k, epi):
-    # 33-256 rows run the decode kernel over row chunks: 64-row chunks, or
-    # 32-row ones where an 8-wave launch of 64-row chunks would need more than
-    # one round of the CUs (n = 6144 at 160 rows); the fused gate/up shape
-    # takes 4 n-tiles per wave.
+    # 33-256 rows: bf16 and residual outputs run the decode kernel over row
+    # chunks (64-row chunks, or 32-row ones where an 8-wave launch of 64-row
+    # chunks would need more than one round of the CUs: n = 6144 at 160
+    # rows); FP32 and the fused gate/up run the panel kernel.
     code = {"bf16": _lib.EPI_BF16, "f32": _lib.EPI_F32, "swiglu": _lib.EPI_SWIGLU, "residual": _lib.EPI_RESIDUAL}[epi]
     got, ref = _gemm_case(m, n, k, code, 31 * m + n + k)
     if epi == "f32":
@@ -292,14 +305,15 @@ def test_gemm_large_m_residual_and_swiglu_epilogues(m):
 
 
 @pytest.mark.parametrize("splits", [0, 1, 3])
-@pytest.mark.parametrize("rows,width", [(1, 1024), (32, 4096), (9, 4096), (100, 1024), (300, 1024)])
+@pytest.mark.parametrize("rows,width", [(1, 1024), (32, 4096), (9, 4096), (100, 1024), (256, 4096), (300, 1024)])
 def test_residual_rmsnorm(splits, rows, width):
-    if splits and rows > 32:
-        pytest.skip("split-K partial slabs hold 32 rows")
+    if splits and rows > 256:
+        pytest.skip("split-K partial slabs hold at most 256 rows")
     r = rng(splits * 100 + rows)
     hidden = rand_bf16(r, rows * width, 2.0)
     w = rand_bf16(r, width, 1.0)
-    slabs = (r.standard_normal((max(splits, 1), 32, width)) * 0.5).astype(np.float32)
+    slab_rows = int(LIB.fh_partial_slab_rows(rows))  # 32 up to 32 rows, else 256
+    slabs = (r.standard_normal((max(splits, 1), slab_rows, width)) * 0.5).astype(np.float32)
     dh, dw_, dp = du.to_dev(hidden), du.to_dev(w), du.to_dev(slabs.reshape(-1))
     dy = du.empty(tiled_rows(rows) * width, np.uint16)
     err = du.empty(1, np.uint32)
@@ -374,9 +388,10 @@ def test_sqrt_rn_is_correctly_rounded_for_every_normal_float():
     assert proc.returncode == 0 and "failures 0" in proc.stdout, proc.stdout + proc.stderr
 
 
-# rows = 260: bf16 rows beyond 256 take the lane-per-(row, head) kernel.
+# rows = 260: bf16 rows beyond 256 take the lane-per-(row, head) kernel;
+# rows = 160 with 5 splits: the wide batches' 256-row partial slabs.
 @pytest.mark.parametrize("qh,kvh,splits,rows", [(32, 8, 0, 9), (16, 8, 0, 9), (32, 8, 1, 9), (32, 8, 3, 9),
-                                                (32, 8, 0, 260)])
+                                                (32, 8, 0, 260), (32, 8, 5, 160)])
 def test_qknorm_rope_kv_bit_exact(qh, kvh, splits, rows):
     r = rng(qh + splits + rows)
     pages, stride, context = 64, 64, 1024
@@ -406,7 +421,7 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh, splits, rows):
         # split-K slabs whose ordered f32 sum is exactly the bf16 value:
         # slab 0 = 2 v, slab 1 = -v (2v - v is exact), rest 0.
         vals = orc.bf16_to_f32(qkv).reshape(rows, ld)
-        slabs = np.zeros((splits, 32, ld), np.float32)
+        slabs = np.zeros((splits, int(LIB.fh_partial_slab_rows(rows)), ld), np.float32)
         if splits == 1:
             slabs[0, :rows] = vals
         else:
