@@ -274,7 +274,7 @@ void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, 
 // consumer adds the slabs in split order.
 //
 // MT: 16-row activation tiles computed (even, >= ceil(m / 16)). Per k-block
-// a wave issues its 2 weight tiles (register loads, LW = 4 k-blocks ahead)
+// a wave issues its 2 weight tiles (register loads, LW = 6 k-blocks ahead)
 // and its share of the panel (XPW direct-to-LDS tile loads, LX k-blocks
 // ahead; the share is uniform, spare loads refetch tile MT - 1 into spare
 // slots). Direct-to-LDS loads and register loads complete out of order with
@@ -283,17 +283,17 @@ void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, 
 // would be the 2 (LW - 1) weight loads after it; if the panel of kb were,
 // the XPW (LX - 1) panel loads after it. Waiting until at most the smaller
 // of the two counts is outstanding covers both. LX is sized per XPW so that
-// the weight count (6) is the smaller one and the weight stream keeps 3
+// the weight count (10) is the smaller one and the weight stream keeps 5
 // k-blocks in flight; with a single count over both kinds (the loads of
 // one k-block assumed complete once all later ones were) the fast panel
 // loads overtook the weight stream and MFMAs read weight registers and
 // panel tiles before they arrived. Measured at 160 rows, cold weights, us
 // per launch (against the 64/32-row launches above): gate/up 24576 x 4096
-// 63 (95), down 4096 x 12288 in 8 splits 29 (56), O 4096 x 4096 in 8 splits
-// 14 (20), QKV 6144 x 4096 in 5 splits 19 (30), LM head 151936 x 4096 271
-// (617). 2 or 8 waves, 4 weight tiles per wave and 1 per wave were slower
-// on every shape.
-constexpr int kPanelWaves = 4, kPanelTilesPerWave = 2, kPanelLW = 4;
+// 55 (95), down 4096 x 12288 in 8 splits 28 (56), O 4096 x 4096 in 8 splits
+// 14 (20), QKV 6144 x 4096 in 5 splits 18 (30), LM head 151936 x 4096 306
+// (617). Weight rings of 4 and 8 k-blocks (gate/up 65, 56), 2 or 8 waves, 4
+// weight tiles per wave and 1 per wave were slower.
+constexpr int kPanelWaves = 4, kPanelTilesPerWave = 2, kPanelLW = 6;
 static_assert(16 * kPanelWaves * kPanelTilesPerWave == kPanelCols, "a workgroup covers kPanelCols weight rows");
 constexpr int panel_xpw(int mt) { return (mt + kPanelWaves - 1) / kPanelWaves; }
 constexpr int panel_lx(int mt) {
