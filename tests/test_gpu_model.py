@@ -580,6 +580,15 @@ def test_prefill_chunk_8b_layer_shapes():
     _prefill_case(cfg, limits, [40], [100, 3000], 64, 37, "prefill 8b")
 
 
+def test_prefill_chunk_of_at_most_32_rows():
+    # 0.6B shape, 2 layers, row capacity 8: a 15-row chunk (a 12-token prompt
+    # beside three decode rows) takes the prefill path with the decode GEMM's
+    # split-K partials (32-row slabs) folded by the norms.
+    cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
+    limits = PagedLimits(context_tokens=1024, physical_page_count=160, page_table_stride=64)
+    _prefill_case(cfg, limits, [12], [50, 300, 7], 32, 53, "prefill 15 rows")
+
+
 def test_prefill_chunk_8b_fused_qkv_epilogue():
     # 8B layer geometry, one layer, 292 rows: above 256 rows the QKV
     # projection runs the 256 x 256-block kernel with QK-norm, RoPE and the KV
