@@ -233,10 +233,14 @@ def test_gemm_split_k_partials(m, n, k, splits):
 
 # 33-256 rows: the panel kernel, one instance per even m-tile count (4 .. 16
 # tiles), slabs of 256 rows; (48, 128, 256, 5): 8 k-blocks in splits of 2, so
-# the fifth split is past the end of k and must write zeros.
+# the fifth split is past the end of k and must write zeros. (42, 4096,
+# 12288, 8) is the 8B down projection at 42 rows, where a wait counting both
+# load kinds together let MFMAs read weight registers and activation tiles
+# before they arrived (tens of thousands of wrong outputs per launch).
 @pytest.mark.parametrize("m,n,k,splits", [(33, 128, 1024, 2), (80, 384, 2048, 3), (100, 6144, 1024, 5),
                                           (160, 1024, 4096, 8), (176, 256, 4096, 4), (200, 256, 2048, 3),
-                                          (256, 128, 1024, 4), (48, 128, 256, 5), (130, 512, 512, 1)])
+                                          (256, 128, 1024, 4), (48, 128, 256, 5), (130, 512, 512, 1),
+                                          (42, 4096, 12288, 8)])
 def test_gemm_wide_split_k_partials(m, n, k, splits):
     got, ref = _gemm_case(m, n, k, _lib.EPI_PARTIAL, 37 * m + splits + n, splits=splits)
     assert np.max(np.abs(got - ref)) <= F32_BOUND
