@@ -14,14 +14,19 @@ void set_thread_error(const char* msg);
 
 // Attention partitions: each partition workgroup covers split_pages pages of
 // 16 tokens (16 or 32; its 8 waves take split_pages / 8 pages each). Batches
-// of at most 64 (row, query head) pairs take 16-page partitions (measured on
-// MI355X, one Qwen3-8B row at a 4096-token context: 13.1 us against 15.7 us
-// for 32 pages, 15.2 us for 8; 4 rows: 32 pages best). attn_split_pages is
-// the one policy every launcher and workspace size uses.
+// of at most 64 (row, query head) pairs, and models of at most 16 query heads
+// (2 per KV head in Qwen3-0.6B, half the work per page of the 8B's 4), take
+// 16-page partitions. Measured on MI355X: one Qwen3-8B row at a 4096-token
+// context 13.1 us against 15.7 us for 32 pages (15.2 us for 8); 4 and 32
+// rows of the 8B: 32 pages best (32 rows, contexts U[512, 8192]: attention
+// 3.63 against 4.29 ms per step with 16); 32 rows of the 0.6B, contexts
+// U[128, 2048]: 0.866 against 0.933 ms per step with 32 (2.04 against 2.12
+// ms per step). attn_split_pages is the one policy every launcher and
+// workspace size uses.
 constexpr uint32_t kAttnMaxSplitPages = 32;
 constexpr uint32_t kAttnMinSplitPages = 16;
 inline uint32_t attn_split_pages(uint32_t rows, uint32_t query_heads) {
-  return (uint64_t)rows * query_heads <= 64 ? 16u : 32u;
+  return (uint64_t)rows * query_heads <= 64 || query_heads <= 16 ? 16u : 32u;
 }
 // Floats per attention partial record: running max, denominator, numerator[128].
 constexpr uint32_t kAttnPartialFloats = 2 + 128;
