@@ -462,12 +462,19 @@ void launch_panel(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n,
 #undef FH_PANEL
 }
 
-// Shape policy (measured on MI355X at m = 32 over the Qwen3-8B projections,
-// cold weights): weights of up to 16K rows use NT = 4 (activation traffic
-// half the weight traffic) with 8 waves, or NT = 3 for split-K partials when
-// only that fills the CUs; the fused gate/up weight (24K rows)
-// keeps NT = 2 with 4 waves, twice as many workgroups in flight; the LM head
-// (152K rows) has n-tiles enough for NT = 4 with 4 waves.
+// Shape policy (measured on MI355X at m = 32, cold weights). Weights of up
+// to 16K rows take the most n-tiles per wave (4, 2, 1) that still give
+// 256 workgroups with the caller's splits (4 keeps the activation traffic
+// at half the weight traffic), or NT = 3 for split-K partials when only
+// that fills the CUs (the 8B QKV weight); the smallest (2 for SwiGLU pairs)
+// when none does. A wave walks at least 4 k-blocks: 8 waves when a split
+// holds 32 k-blocks or more, else 4. The 8B projections keep NT = 4 (3 for
+// QKV) with 8 waves; the Qwen3-0.6B ones, too small to fill the CUs with 4,
+// went (us per launch, 32 rows) from QKV 6.2 to 4.1 (NT 2, 4 waves), O 6.0
+// to 3.3-4.2 (NT 1), gate/up 6.7 to 5.1 (NT 2, 8 waves), down 6.1 to 4.2
+// (NT 1). The fused 8B gate/up weight (24K rows) keeps NT = 2 with 4 waves,
+// twice as many workgroups in flight; the LM head (152K rows) has n-tiles
+// enough for NT = 4 with 4 waves.
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
@@ -499,8 +506,24 @@ void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, u
       return;
     }
   }
-  if (n % 64 == 0 && n < 16384) {
-    launch_variant<4, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
+  if (n < 16384) {
+    const bool eight = (k / 32 + splits - 1) / splits >= 32;
+    auto fills = [&](uint32_t nt) { return n % (16 * nt) == 0 && n / (16 * nt) * splits >= 256; };
+#define FH_VARIANT(NT_)                                                                    \
+  do {                                                                                     \
+    if (eight)                                                                             \
+      launch_variant<NT_, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s); \
+    else                                                                                   \
+      launch_variant<NT_, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s); \
+  } while (0)
+    if (fills(4)) {
+      FH_VARIANT(4);
+    } else if (n % 32 == 0 && (fills(2) || EPI == FH_EPI_SWIGLU)) {
+      FH_VARIANT(2);
+    } else if constexpr (EPI != FH_EPI_SWIGLU) {
+      FH_VARIANT(1);
+    }
+#undef FH_VARIANT
   } else if (EPI != FH_EPI_SWIGLU && n % 64 == 0) {
     launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
   } else if (n % 32 == 0) {
