@@ -140,6 +140,7 @@ SIGNATURES = [
     ("fh_op_synth_fill", _st, [_vp, _u64, _u64, ctypes.c_float, _vp]),
     ("fh_speculative_token_assembly", _st, [_u32p, _u32p, _u32, _u32, _u32p]),
     ("fh_verify_greedy_round", _st, [_u32p, _u32, _u32p, _u32, _u32p, _u32p, _u32p]),
+    ("fh_verify_greedy_batch", _st, [_u32p, _u32p, _u32, _u32, _u32p, _u32p]),
     ("fh_compact_completion", _st, [_u32p, _u32p, _u32p, _u32p, _u32p, _u64p, ctypes.POINTER(ctypes.c_uint8), _u32,
                                     _u32, _u32, ctypes.POINTER(ctypes.c_uint8)]),
 ]

@@ -375,4 +375,22 @@ fh_status fh_verify_greedy_round(const uint32_t* draft, uint32_t draft_count, co
   return FH_OK;
 }
 
+fh_status fh_verify_greedy_batch(const uint32_t* draft, const uint32_t* target, uint32_t sequences, uint32_t k,
+                                 uint32_t* accepted, uint32_t* emitted) {
+  if (sequences == 0) return FH_OK;
+  if (!target || !accepted || !emitted || (k && !draft)) return FH_ERR_INVALID_ARGUMENT;
+  if (k == 0xffffffffu) return FH_ERR_INVALID_ARGUMENT;  // DraftTokenCountOverflow
+  const uint64_t stride = (uint64_t)k + 1;
+  for (uint32_t s = 0; s < sequences; ++s) {
+    const uint32_t* t = target + s * stride;
+    uint32_t* e = emitted + s * stride;
+    uint32_t a = 0;
+    while (a < k && draft[(uint64_t)a * sequences + s] == t[a]) ++a;
+    for (uint32_t i = 0; i < a; ++i) e[i] = draft[(uint64_t)i * sequences + s];
+    e[a] = t[a];
+    accepted[s] = a;
+  }
+  return FH_OK;
+}
+
 }  // extern "C"

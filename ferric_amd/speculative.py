@@ -90,6 +90,23 @@ def verify_greedy(draft, target):
     return int(acc.value), [int(x) for x in em[: n.value]]
 
 
+def verify_greedy_batch(draft_iteration_major, target):
+    """verify_greedy for every sequence of a round in one C call: draft [K][S],
+    target [S][K + 1]; returns (accepted [S], emitted [S][K + 1]) with the
+    first accepted[s] + 1 entries of emitted[s] meaningful."""
+    lib = load()
+    t, tp = _u32(np.asarray(target, dtype=np.uint32).reshape(-1))
+    s = int(np.asarray(target).shape[0])
+    k = t.size // s - 1 if s else 0
+    d, dp = _u32(np.asarray(draft_iteration_major, dtype=np.uint32).reshape(-1) if k else [0])
+    accepted = np.zeros(max(s, 1), dtype=np.uint32)
+    emitted = np.zeros(max(s * (k + 1), 1), dtype=np.uint32)
+    check(lib.fh_verify_greedy_batch(dp if k else None, tp, s, k,
+                                     accepted.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                     emitted.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))))
+    return accepted[:s], emitted[: s * (k + 1)].reshape(s, k + 1)
+
+
 def compact_completion(choices, draft, active_lengths, slots, generations, epochs, plans, active_tokens, k):
     """Per-sequence completion records (list of 120-byte strings) of
     fh_compact_completion: choices [S][active_tokens], draft [K][S]
@@ -185,8 +202,10 @@ class SpeculativeDecoder:
                                          [self.plan] * n, k + 1, k)
         self.epoch += 1
         accepted, emitted = [], []
+        acc, ems = verify_greedy_batch(draft, choices)
         for j, s in enumerate(seqs):
-            a, em = verify_greedy(draft[:, j], choices[j])
+            a = int(acc[j])
+            em = [int(x) for x in ems[j, : a + 1]]
             c = s.cursor
             self.tpool.truncate(s.target_sid, c + a + 1)
             self.dpool.truncate(s.draft_sid, c + min(a + 1, k))

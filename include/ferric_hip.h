@@ -330,6 +330,13 @@ fh_status fh_speculative_token_assembly(const uint32_t* anchors, const uint32_t*
 fh_status fh_verify_greedy_round(const uint32_t* draft, uint32_t draft_count, const uint32_t* target,
                                  uint32_t target_count, uint32_t* accepted, uint32_t* emitted,
                                  uint32_t* emitted_count);
+/* fh_verify_greedy_round for every sequence of a round in one call: draft is iteration-major
+ * [k][sequences] (as fh_speculative_token_assembly takes it), target is [sequences][k + 1] (the
+ * verify batch's choices); accepted[s] and emitted[s][0 .. accepted[s]] as for one sequence.
+ * No counterpart in the reference, which settles sequence by sequence (speculation.rs:126);
+ * for callers that settle a whole round at once. */
+fh_status fh_verify_greedy_batch(const uint32_t* draft, const uint32_t* target, uint32_t sequences, uint32_t k,
+                                 uint32_t* accepted, uint32_t* emitted);
 
 /* Per-sequence 120-byte completion records [sequences][120] of
  * ferric_qwen3_compact_completion_v1 (device/qwen3-all-kernels-v1/src/logits.rs:279):

@@ -69,6 +69,28 @@ def test_verify_greedy_round_matches_the_reference_vectors():
     assert lib.fh_verify_greedy_round(None, 0, None, 0, ctypes.byref(a), e, ctypes.byref(n)) == 1
 
 
+def test_verify_greedy_batch_settles_each_sequence_like_the_single_call():
+    # Every sequence of a round in one call (draft iteration-major [K][S],
+    # target [S][K + 1]) against the oracle's per-sequence verify: random
+    # rounds over a 3-token alphabet (every acceptance count occurs), K = 0,
+    # and the three reference vectors as one round.
+    from ferric_amd.speculative import verify_greedy_batch
+    lib = ferric_amd.load()
+    r = np.random.default_rng(9)
+    cases = [(r.integers(0, 3, (k, s)), r.integers(0, 3, (s, k + 1))) for k, s in [(4, 32), (1, 5), (7, 3), (0, 4)]]
+    cases.append((np.array([[3, 3, 3], [4, 4, 4], [5, 5, 5]]), np.array([[9, 4, 5, 6], [3, 4, 9, 6], [3, 4, 5, 6]])))
+    for draft, target in cases:
+        acc, ems = verify_greedy_batch(draft, target)
+        for s in range(target.shape[0]):
+            want_a, want_e = orc.verify_greedy([int(x) for x in draft[:, s]], [int(x) for x in target[s]])
+            assert int(acc[s]) == want_a and [int(x) for x in ems[s, : want_a + 1]] == want_e, (s, draft, target)
+    e, acc = (ctypes.c_uint32 * 8)(), (ctypes.c_uint32 * 2)()
+    assert lib.fh_verify_greedy_batch(None, u32([1, 2]), 2, 0, acc, e) == 0  # K = 0: the bonus token only
+    assert list(e[:2]) == [1, 2] and list(acc) == [0, 0]
+    assert lib.fh_verify_greedy_batch(None, u32([1, 2, 3, 4]), 2, 1, acc, e) == 1  # draft missing
+    assert lib.fh_verify_greedy_batch(None, None, 0, 4, None, None) == 0  # no sequences
+
+
 def test_token_assembly_matches_the_oracle():
     lib = ferric_amd.load()
     r = np.random.default_rng(0)
