@@ -133,6 +133,8 @@ SIGNATURES = [
     ("fh_op_qknorm_rope_kv", _st, [_vp, _u32] + [_vp] * 9 + [_u32] * 6 + [ctypes.c_float, _vp, _vp]),
     ("fh_attention_scratch_bytes", _u64, [_u32, _u32, _u32]),
     ("fh_op_paged_attention", _st, [_vp] * 6 + [_u32, _vp] + [_u32] * 6 + [_vp, _vp]),
+    ("fh_op_qknorm_paged_attention", _st,
+     [_vp, _u32] + [_vp] * 9 + [_u32, _vp] + [_u32] * 6 + [ctypes.c_float, _vp, _vp]),
     ("fh_op_paged_attention_noalloc", _st, [_vp] * 6 + [_u32] * 7 + [_vp, _vp]),
     ("fh_op_swiglu", _st, [_vp, _vp, _vp, _u64, _vp, _vp]),
     ("fh_argmax_scratch_bytes", _u64, [_u32]),

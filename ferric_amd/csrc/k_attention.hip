@@ -131,18 +131,55 @@ __device__ __forceinline__ void merge_records(const float* p, uint32_t ns, int l
 // issues all of its V loads at once: two memory round trips per wave.
 // FUSED: counters[r * kvh + h] counts the finished partitions of a
 // multi-partition (row, KV head); the one that finishes last merges.
-template <int G, int WAVES, int PP, bool FUSED>
+// QKS > 0: the QK-norm + RoPE + KV append stage runs here (AttnQkn): q is
+// formed from QKS split-K slabs of the QKV projection instead of read from
+// `q`, and the new token's K/V are formed, appended and used in place of
+// the cache's slot.
+template <int G, int WAVES, int PP, bool FUSED, int QKS>
 __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, float* __restrict__ part,
     uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t row0, uint32_t qh, uint32_t kvh, uint32_t stride,
-    uint32_t pages, uint32_t context, uint32_t smax, uint32_t* counters, uint32_t* err) {
+    uint32_t pages, uint32_t context, uint32_t smax, uint32_t* counters, uint32_t* err, AttnQkn qk) {
   constexpr uint32_t kWavePages = PP / WAVES;
   static_assert(PP % WAVES == 0 && kWavePages >= 1, "pages split evenly over the waves");
+  constexpr bool kQkn = QKS > 0;
+  static_assert(!kQkn || G + 2 <= WAVES, "one wave per query head, one for the key and one for the value head");
+  // With at most two pages per wave the V registers fit beside K's, so V is
+  // requested together with K (one memory round trip instead of two).
+  constexpr bool kEarlyV = kQkn && kWavePages <= 2;
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
   // The wave index is uniform; saying so keeps every page address scalar.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t p0 = split * PP;
+
+  // Fused QK-norm, part 1. Wave w < G forms query head h G + w, wave G the
+  // key head and wave G + 1 the value head of KV head h (lane l: elements l
+  // and l + 64). Their slab and norm-weight loads go out first: a wave's
+  // loads complete in issue order, so anything requested after the K loads
+  // could only be used once K has landed.
+  const int qk_role = kQkn && wave < G + 2 ? wave : -1;
+  float qk_a[kQkn ? QKS : 1], qk_b[kQkn ? QKS : 1];
+  uint32_t qk_wa = 0u, qk_wb = 0u;
+  if constexpr (kQkn) {
+    // Every wave issues these (the ones without a head re-read query head
+    // h G): loads under a branch would be joined with the branch's other
+    // side right here, which makes the wave wait for them.
+    const int role = qk_role >= 0 ? qk_role : 0;
+    const uint32_t ld = (qh + 2 * kvh) * 128;
+    const uint32_t head = role < G ? h * G + role : (role == G ? qh + h : qh + kvh + h);
+    const float* pp = qk.qkv_part + (uint64_t)r * ld + head * 128 + lane;
+    const uint64_t slab = (uint64_t)qk.slab_rows * ld;
+#pragma unroll
+    for (int sp = 0; sp < QKS; ++sp) {
+      qk_a[sp] = pp[sp * slab];
+      qk_b[sp] = pp[sp * slab + 64];
+    }
+    const uint16_t* wn = role < G ? qk.q_norm : qk.k_norm;  // (the value head's go unused)
+    qk_wa = wn[lane];  // widened where used: converting here would wait for the load
+    qk_wb = wn[lane + 64];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   // This wave's pages: [w0, w0 + np) of the row. The page-table entries are
   // requested together with the position (they do not depend on it), so the
   // K loads wait for one memory round trip, not two.
@@ -152,7 +189,9 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   const uint32_t raw_phys = lane < (int)kWavePages && w0 + lane < stride ? trow[w0 + lane] : 0u;
   const uint32_t pos = positions[r];
   if (pos >= context || pos / 16 >= stride) {
-    if (split == 0 && h == 0 && threadIdx.x == 0) raise_error(err, ERR_POSITION);
+    // (The separate QK-norm kernel reports this row's missing KV slot as a
+    // page fault; the fused form reports both.)
+    if (split == 0 && h == 0 && threadIdx.x == 0) raise_error(err, kQkn ? (ERR_POSITION | ERR_PAGE) : ERR_POSITION);
     return;
   }
   const uint32_t ctx = pos + 1;
@@ -160,6 +199,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   if (p0 >= row_pages) return;  // uniform per workgroup
   const uint32_t nsplit = (row_pages + PP - 1) / PP;
   const uint32_t np = w0 < row_pages ? min(row_pages - w0, kWavePages) : 0u;
+  // Fused: the last partition holds the new token (page pos / 16, slot
+  // pos % 16); the wave whose pages include it appends and uses the new K/V.
+  const bool last_part = split == nsplit - 1;
+  const uint32_t upos = pos / 16 - w0;  // page index within this wave when it owns the token
+  const bool own_pos = kQkn && last_part && pos / 16 >= w0 && upos < np;
+  const uint32_t epos = pos & 15u;
 
   // Scores of the wave's tokens, replaced in place by probabilities: [token][g].
   __shared__ float sbuf[WAVES][kWavePages * 16][G];
@@ -175,13 +220,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   // B operand: query head h*G + r16 (zero for r16 >= G); MFMA i, lane group
   // g16 covers dims 32*i + 8*g16 .. +7.
   u32x4 qv[4];
-  if (r16 < G) {
-    const uint16_t* qp = q + ((uint64_t)r * qh + h * G + r16) * 128 + 8 * g16;
+  if constexpr (!kQkn) {
+    if (r16 < G) {
+      const uint16_t* qp = q + ((uint64_t)r * qh + h * G + r16) * 128 + 8 * g16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
-  } else {
+      for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   // Physical pages of this wave, one per lane, read back with readlane so no
@@ -195,12 +242,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   // and each query head's maximum over the wave's tokens.
   const uint32_t vstride = kvh * 64;  // dwords between consecutive slots of one head
   uint32_t vd[kWavePages][16];
-  auto load_v = [&] {
+  // ALL: as load_k below.
+  auto load_v = [&](auto all_tag) {
+    constexpr bool ALL = decltype(all_tag)::value;
+    const uint32_t spare = np ? phys_of(0) : 0u;
 #pragma unroll
     for (uint32_t u = 0; u < kWavePages; ++u) {
-      if (u < np) {
-        const uint32_t* vp =
-            reinterpret_cast<const uint32_t*>(vc + (((uint64_t)phys_of(u) * 16) * kvh + h) * 128) + lane;
+      if (ALL || u < np) {
+        const uint32_t pu = ALL && u >= np ? spare : phys_of(u);
+        const uint32_t* vp = reinterpret_cast<const uint32_t*>(vc + (((uint64_t)pu * 16) * kvh + h) * 128) + lane;
 #pragma unroll
         for (int e = 0; e < 16; ++e) vd[u][e] = __builtin_nontemporal_load(vp + e * vstride);
       }
@@ -225,24 +275,101 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
       if (r16 < G) sw[(t + e) * G + r16] = sv;
     }
   };
+  // Fused: the formed heads (bf16): query heads 0..G-1, then the new K and V.
+  __shared__ __align__(16) uint32_t qkn_s[kQkn ? G + 2 : 1][64];
   {
     // Whole 256-byte token rows per load (lane: token 4 i + g16, dims
     // 8 r16 .. 8 r16 + 7), turned into the A-operand layout through a padded
     // LDS tile (272-byte rows keep the column reads conflict-free).
     __shared__ u32x4 ktile[WAVES][16][17];
     u32x4 kr[kWavePages][4];
+    // ALL: issue a load for every page slot of the wave, pages past the
+    // context re-reading the wave's first page (or page 0), so the number of
+    // loads in flight is the same on every path and a wait for an earlier
+    // load does not also wait for these.
+    auto load_k = [&](auto all_tag) {
+      constexpr bool ALL = decltype(all_tag)::value;
+      const uint32_t spare = np ? phys_of(0) : 0u;
 #pragma unroll
-    for (uint32_t u = 0; u < kWavePages; ++u) {
-      if (u < np) {
-        const uint16_t* kp = kc + (((uint64_t)phys_of(u) * 16 + g16) * kvh + h) * 128 + 8 * r16;
+      for (uint32_t u = 0; u < kWavePages; ++u) {
+        if (ALL || u < np) {
+          const uint32_t pu = ALL && u >= np ? spare : phys_of(u);
+          const uint16_t* kp = kc + (((uint64_t)pu * 16 + g16) * kvh + h) * 128 + 8 * r16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          kr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128));
+          for (int i = 0; i < 4; ++i)
+            kr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (uint64_t)4 * i * kvh * 128));
+        }
       }
+    };
+    if constexpr (kQkn) {
+      if (qk_role >= 0) {
+        // Fused QK-norm, part 2 (the decode QK-norm kernel's arithmetic, the
+        // same routine): RoPE factors at the position, then this wave's K
+        // (and V) loads, then fold the slabs in split order, round, and
+        // normalize and rotate (query and key heads) or keep raw (value).
+        const float qk_c = qk.cos_t[(uint64_t)pos * 64 + lane];
+        const float qk_s = qk.sin_t[(uint64_t)pos * 64 + lane];
+        load_k(std::true_type{});
+        if constexpr (kEarlyV) load_v(std::true_type{});
+        __builtin_amdgcn_sched_barrier(0);
+        if (qk_role < G || last_part) {
+          float a = qk_a[0], b = qk_b[0];
+#pragma unroll
+          for (int sp = 1; sp < QKS; ++sp) {
+            a += qk_a[sp];
+            b += qk_b[sp];
+          }
+          a = round_bf16(a);
+          b = round_bf16(b);
+          uint32_t ra, rb;
+          if (qk_role <= G) {
+            bad |= qknorm_rope_wave_head(a, b, bf16_to_f32(qk_wa), bf16_to_f32(qk_wb), qk_c, qk_s, qk.eps, ra, rb);
+          } else {
+            ra = f32_to_bf16(a);
+            rb = f32_to_bf16(b);
+          }
+          uint16_t* row_s = reinterpret_cast<uint16_t*>(&qkn_s[qk_role][0]);
+          row_s[lane] = (uint16_t)ra;
+          row_s[lane + 64] = (uint16_t)rb;
+        }
+      } else {
+        load_k(std::false_type{});
+        if constexpr (kEarlyV) load_v(std::false_type{});
+      }
+      __syncthreads();
+      if (r16 < G) {
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(&qkn_s[r16][0]) + 8 * g16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+      if (own_pos) {
+        // Append the new token's K and V at (pages[pos / 16], pos % 16), as
+        // the decode QK-norm kernel does (nothing is written to a page
+        // outside the pool; that page is reported below).
+        const uint32_t phys = __builtin_amdgcn_readlane((int)raw_phys, (int)upos);
+        if (phys < pages) {
+          const uint64_t slot = ((uint64_t)phys * 16 + epos) * kvh + h;
+          reinterpret_cast<uint32_t*>(qk.k_cache + slot * 128)[lane] = qkn_s[G][lane];
+          reinterpret_cast<uint32_t*>(qk.v_cache + slot * 128)[lane] = qkn_s[G + 1][lane];
+        }
+      }
+    } else {
+      load_k(std::false_type{});
     }
 #pragma unroll
     for (uint32_t u = 0; u < kWavePages; ++u) {
       if (u < np) {
+        if constexpr (kQkn) {
+          // The new token's K replaces whatever its slot held.
+          if (own_pos && u == upos) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (4 * i + g16 == (int)epos) kr[u][i] = *reinterpret_cast<const u32x4*>(&qkn_s[G][4 * r16]);
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) ktile[wave][4 * i + g16][r16] = kr[u][i];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -259,7 +386,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     }
   }
   // V loads go out now, so they are in flight during the softmax.
-  load_v();
+  if constexpr (!kEarlyV) load_v(std::false_type{});
   pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
   pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
   float m[G], l[G], acc[G][2];
@@ -295,6 +422,19 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
 
   // Pass 2: n += p * v on VALU; lane l owns output dims 2l, 2l+1, and a
   // token's V row is one coalesced 256-byte wave load.
+  if constexpr (kQkn) {
+    if (own_pos) {
+      // The new token's V replaces whatever its slot held.
+      const uint32_t vn = qkn_s[G + 1][lane];
+#pragma unroll
+      for (uint32_t u = 0; u < kWavePages; ++u)
+        if (u == upos) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if ((uint32_t)e == epos) vd[u][e] = vn;
+        }
+    }
+  }
   {
     auto pv_page = [&](auto full_tag, uint32_t u) {
       constexpr bool FULL = decltype(full_tag)::value;
@@ -436,40 +576,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(const float* _
   if (!(L > 0.f) || ((o0 & 0x7f80u) == 0x7f80u) || ((o1 & 0x7f80u) == 0x7f80u)) raise_error(err, ERR_NONFINITE);
 }
 
-template <int G, int PP, bool FUSED>
+template <int G, int PP, bool FUSED, int QKS>
 void launch_partition(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                       const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
                       uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                      uint32_t smax, uint32_t* counters, uint32_t* err, hipStream_t s) {
+                      uint32_t smax, uint32_t* counters, uint32_t* err, const AttnQkn& qk, hipStream_t s) {
   constexpr int kWaves = 8;
-  hipLaunchKernelGGL((attn_partition_kernel<G, kWaves, PP, FUSED>), dim3(smax, kvh, rows), dim3(64 * kWaves), 0, s,
-                     q, kc, vc, positions, table, part, out, out_mtiles, row0, qh, kvh, stride, pages, context, smax,
-                     counters, err);
+  hipLaunchKernelGGL((attn_partition_kernel<G, kWaves, PP, FUSED, QKS>), dim3(smax, kvh, rows), dim3(64 * kWaves), 0,
+                     s, q, kc, vc, positions, table, part, out, out_mtiles, row0, qh, kvh, stride, pages, context, smax,
+                     counters, err, qk);
 }
 
-template <int G, int PP>
+template <int G, int PP, int QKS>
 void launch_partition_pp(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                          const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
                          uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                         uint32_t smax, uint32_t* counters, uint32_t* err, hipStream_t s) {
+                         uint32_t smax, uint32_t* counters, uint32_t* err, const AttnQkn& qk, hipStream_t s) {
   if (counters)
-    launch_partition<G, PP, true>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride,
-                                  pages, context, smax, counters, err, s);
+    launch_partition<G, PP, true, QKS>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh,
+                                       stride, pages, context, smax, counters, err, qk, s);
   else
-    launch_partition<G, PP, false>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride,
-                                   pages, context, smax, counters, err, s);
+    launch_partition<G, PP, false, QKS>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh,
+                                        stride, pages, context, smax, counters, err, qk, s);
 }
 
-template <int G>
+template <int G, int QKS>
 hipError_t launch_partition_g(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const uint32_t* positions,
                               const uint32_t* table, float* part, uint16_t* out, uint32_t out_mtiles, uint32_t row0,
                               uint32_t rows, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
                               uint32_t context, uint32_t split_pages, uint32_t* counters, uint32_t* err,
-                              hipStream_t s) {
+                              const AttnQkn& qk, hipStream_t s) {
   const uint32_t smax = attn_max_splits(context, split_pages);
   switch (split_pages) {
-    case 16: launch_partition_pp<G, 16>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, s); break;
-    case 32: launch_partition_pp<G, 32>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, s); break;
+    case 16: launch_partition_pp<G, 16, QKS>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, qk, s); break;
+    case 32: launch_partition_pp<G, 32, QKS>(q, kc, vc, positions, table, part, out, out_mtiles, row0, rows, qh, kvh, stride, pages, context, smax, counters, err, qk, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
@@ -477,19 +617,35 @@ hipError_t launch_partition_g(const uint16_t* q, const uint16_t* kc, const uint1
 
 }  // namespace
 
+bool attention_qkn_supported(uint32_t qh, uint32_t kvh, uint32_t qkv_splits) {
+  return kvh && qh % kvh == 0 && qh / kvh <= 4 && (qh / kvh & (qh / kvh - 1)) == 0 && qkv_splits == 2;
+}
+
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
                                     uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
                                     uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s) {
+                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s,
+                                    const AttnQkn* qkn) {
   const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   hipError_t e;
-  switch (qh / kvh) {
-    case 1: e = launch_partition_g<1>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
-    case 2: e = launch_partition_g<2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
-    case 4: e = launch_partition_g<4>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
-    case 8: e = launch_partition_g<8>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, s); break;
-    default: return hipErrorInvalidValue;
+  const AttnQkn none{};
+  if (qkn) {
+    if (!attention_qkn_supported(qh, kvh, qkn->splits) || row0 != 0) return hipErrorInvalidValue;
+    switch (qh / kvh) {
+      case 1: e = launch_partition_g<1, 2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, *qkn, s); break;
+      case 2: e = launch_partition_g<2, 2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, *qkn, s); break;
+      case 4: e = launch_partition_g<4, 2>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, *qkn, s); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (qh / kvh) {
+      case 1: e = launch_partition_g<1, 0>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, none, s); break;
+      case 2: e = launch_partition_g<2, 0>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, none, s); break;
+      case 4: e = launch_partition_g<4, 0>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, none, s); break;
+      case 8: e = launch_partition_g<8, 0>(q, k_cache, v_cache, positions, table, partials, out, mt, row0, rows, qh, kvh, stride, pages, context, split_pages, counters, err, none, s); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   if (e != hipSuccess) return e;
   return hipGetLastError();

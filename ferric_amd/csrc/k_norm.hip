@@ -166,25 +166,11 @@ __global__ __launch_bounds__(kHeadsPerGroup * 64) void qknorm_rope_kv_kernel(
     return;
   }
 
-  bool bad = !is_finite_f32(a) | !is_finite_f32(b);
-  const float sqa = a * a, sqb = b * b;
-  float sum = 0.f;
-#pragma unroll
-  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqa, l);
-#pragma unroll
-  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqb, l);
-  const float inv = inverse_rms(sum, 128.0f, eps);
-  bad |= !is_finite_f32(sum) | !is_finite_f32(inv);
-
   const uint16_t* wn = head < qh ? q_norm : k_norm;
-  const float an = bf16_to_f32(norm_weight_bf16(a, inv, bf16_to_f32(wn[lane])));
-  const float bn = bf16_to_f32(norm_weight_bf16(b, inv, bf16_to_f32(wn[lane + 64])));
   const uint32_t trig = (pos < context ? pos : 0) * 64 + lane;
-  const float c = cos_t[trig], s = sin_t[trig];
-  const float a_cos = an * c, b_sin = bn * s, b_cos = bn * c, a_sin = an * s;
-  const uint32_t ra = f32_to_bf16(a_cos - b_sin);
-  const uint32_t rb = f32_to_bf16(b_cos + a_sin);
-  bad |= ((ra & 0x7f80u) == 0x7f80u) | ((rb & 0x7f80u) == 0x7f80u);
+  uint32_t ra, rb;
+  const bool bad = qknorm_rope_wave_head(a, b, bf16_to_f32(wn[lane]), bf16_to_f32(wn[lane + 64]), cos_t[trig],
+                                         sin_t[trig], eps, ra, rb);
   uint16_t* dst = nullptr;
   if (head < qh)
     dst = q_out + ((uint64_t)row * qh + head) * 128;

@@ -140,11 +140,34 @@ uint32_t gemm_panel_splits(uint32_t n, uint32_t k);
 // launch_attention_merge (same split_pages). counters != nullptr: rows x kvh
 // words, zero on entry and left zero; the last partition of each (row, KV
 // head) to finish merges that pair's records itself, in the same launch.
+//
+// qkn != nullptr (decode, row0 == 0): the partition kernel also runs the
+// QK-norm + RoPE + KV append stage (launch_qknorm_rope_kv's arithmetic, bit
+// for bit): every partition forms its query heads from the QKV projection's
+// split-K slabs (q is not read), and the partition holding a row's new token
+// appends that token's K/V to the caches and uses them. The caller must make
+// sure no row reads a slot that another row of the launch writes (each row's
+// written page listed by that row only). attention_qkn_supported() gives
+// the shapes it covers (at most 4 query heads per KV head, 2 slabs).
+struct AttnQkn {
+  const float* qkv_part;  // splits slabs of [slab_rows][(qh + 2 kvh) * 128] FP32
+  uint32_t splits;
+  uint32_t slab_rows;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  const float* cos_t;  // [context][64]
+  const float* sin_t;
+  uint16_t* k_cache;  // written: the new token's slot
+  uint16_t* v_cache;
+  float eps;
+};
+bool attention_qkn_supported(uint32_t qh, uint32_t kvh, uint32_t qkv_splits);
 hipError_t launch_attention_partial(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                     const uint32_t* positions, const uint32_t* table, float* partials, uint16_t* out,
                                     uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
                                     uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s);
+                                    uint32_t split_pages, uint32_t* counters, uint32_t* err, hipStream_t s,
+                                    const AttnQkn* qkn = nullptr);
 hipError_t launch_attention_merge(const float* partials, const uint32_t* positions, uint16_t* out,
                                   uint32_t out_tiled, uint32_t row0, uint32_t out_rows, uint32_t rows, uint32_t qh,
                                   uint32_t context, uint32_t split_pages, uint32_t* err, hipStream_t s);

@@ -220,6 +220,33 @@ uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_
          fh::attn_max_splits(context_tokens, fh::attn_split_pages(rows, query_heads)) * fh::kAttnPartialFloats * 4;
 }
 
+fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_splits, const uint16_t* q_norm,
+                                       const uint16_t* k_norm, const float* cos_table, const float* sin_table,
+                                       const uint32_t* positions, const uint32_t* page_table, uint16_t* k_cache,
+                                       uint16_t* v_cache, uint16_t* out, uint32_t out_tiled, void* scratch,
+                                       uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
+                                       uint32_t physical_pages, uint32_t context_tokens, float epsilon,
+                                       uint32_t* error_word, void* stream) {
+  if (!qkv_partials || !q_norm || !k_norm || !cos_table || !sin_table || !positions || !page_table || !k_cache ||
+      !v_cache || !out || !scratch || rows == 0 || rows > fh::kMaxRows || stride == 0 || physical_pages == 0 ||
+      context_tokens == 0 || (uint64_t)stride * 16 < context_tokens ||
+      !fh::attention_qkn_supported(query_heads, kv_heads, qkv_splits))
+    return FH_ERR_INVALID_ARGUMENT;
+  hipStream_t s = as_stream(stream);
+  float* part = reinterpret_cast<float*>(scratch);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
+  const fh::AttnQkn qa{qkv_partials, qkv_splits, fh::partial_slab_rows(rows), q_norm, k_norm, cos_table, sin_table,
+                       k_cache,      v_cache,    epsilon};
+  (void)hipGetLastError();
+  hipError_t e = fh::launch_attention_partial(nullptr, k_cache, v_cache, positions, page_table, part, out, out_tiled,
+                                              0, rows, rows, query_heads, kv_heads, stride, physical_pages,
+                                              context_tokens, split_pages, nullptr, error_word, s, &qa);
+  if (e == hipSuccess)
+    e = fh::launch_attention_merge(part, positions, out, out_tiled, 0, rows, rows, query_heads, context_tokens,
+                                   split_pages, error_word, s);
+  return status_of(e);
+}
+
 fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                 const uint32_t* positions, const uint32_t* page_table, uint16_t* out,
                                 uint32_t out_tiled, void* scratch, uint32_t rows, uint32_t query_heads,

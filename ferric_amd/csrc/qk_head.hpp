@@ -65,6 +65,35 @@ __device__ __forceinline__ uint32_t norm_weight_bf16_int(float x, float inv, flo
   return f32_to_bf16_int(normalized * w);
 }
 
+// QK-norm + RoPE of one normalized head held by a wave: lane l holds
+// elements l (a) and l + 64 (b) as bf16-valued floats, wa/wb the norm
+// weights of those elements, c/s the RoPE factors of pair l at the row's
+// position. The square sum runs serially in element order 0..127 (one
+// rounding per square and per add, rmsnorm.rs:421-438) through lane reads.
+// ra/rb: the rotated bf16 outputs of elements l and l + 64. Returns true
+// when a value or the sum is nonfinite. The decode QK-norm kernel and the
+// decode attention kernel's fused form both call this, so their outputs are
+// bit-identical.
+__device__ __forceinline__ bool qknorm_rope_wave_head(float a, float b, float wa, float wb, float c, float s,
+                                                      float eps, uint32_t& ra, uint32_t& rb) {
+  bool bad = !is_finite_f32(a) | !is_finite_f32(b);
+  const float sqa = a * a, sqb = b * b;
+  float sum = 0.f;
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqa, l);
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqb, l);
+  const float inv = inverse_rms(sum, 128.0f, eps);
+  bad |= !is_finite_f32(sum) | !is_finite_f32(inv);
+  const float an = bf16_to_f32(norm_weight_bf16(a, inv, wa));
+  const float bn = bf16_to_f32(norm_weight_bf16(b, inv, wb));
+  const float a_cos = an * c, b_sin = bn * s, b_cos = bn * c, a_sin = an * s;
+  ra = f32_to_bf16(a_cos - b_sin);
+  rb = f32_to_bf16(b_cos + a_sin);
+  bad |= ((ra & 0x7f80u) == 0x7f80u) | ((rb & 0x7f80u) == 0x7f80u);
+  return bad;
+}
+
 struct QkvRopeArgs {
   const uint16_t* q_norm;
   const uint16_t* k_norm;

@@ -152,9 +152,12 @@ struct fh_ctx {
     uint32_t logical = 0;
     uint32_t row = 0;
     uint32_t conflict = 0;
+    uint32_t multi = 0;  // listed by more than one row of the batch
   };
   std::vector<PageOwner> page_owner;
   std::vector<uint8_t> row_dup;  // per row of the batch: a page listed twice
+  bool batch_private_slots = false;  // no row lists a page another row of the batch writes
+  bool last_qkn = false;             // the last decode step ran QK-norm/KV append inside attention
   std::vector<uint64_t> slot_scratch;
   uint64_t stamp = 0;
 };
@@ -325,8 +328,10 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
         o.sequence = r.sequence;
         o.logical = j;
         o.conflict = 0;
+        o.multi = 0;
       } else {
         row_dup |= o.row == i;
+        o.multi |= o.row != i;
         if (o.sequence != r.sequence || o.logical != j) o.conflict = 1;
       }
       o.row = i;
@@ -348,6 +353,12 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
     if (o.conflict || o.sequence != r.sequence || o.logical != logical)
       return fail(ctx, FH_ERR_SHARED_PAGE, "batch writes a page shared with another sequence or logical position");
   }
+  // A row may read another row's new slot only where that row's written
+  // page is listed by another row (rows of one sequence in one batch); the
+  // decode step then keeps the QK-norm/KV append as a launch of its own.
+  ctx->batch_private_slots = true;
+  for (uint32_t i = 0; i < nrows; ++i)
+    if (owner[rows[i].writable_page].multi) ctx->batch_private_slots = false;
   std::sort(slots.begin(), slots.end());
   if (std::adjacent_find(slots.begin(), slots.end()) != slots.end())
     return fail(ctx, FH_ERR_INVALID_ROW, "invalid paged row geometry or aliased write slot");
@@ -389,6 +400,31 @@ struct Enq {
   }
 };
 
+// Whether this decode batch runs the QK-norm/RoPE/KV append inside the
+// attention partitions: every row's written page private to that row, a
+// model shape the fused kernel covers, and a launch small enough to merge
+// its partitions in the same launch (attn_fuse_merge). Each partition then
+// forms its query heads itself, and the serial square sum of the norm (128
+// dependent adds per head) sits before its scores. Measured on MI355X
+// (alternating runs on one GPU, graph replays): one Qwen3-8B row at a
+// 4096-token context 3.538 -> 3.467-3.483 ms per step; 32 rows of the 8B at
+// contexts U[512, 8192] 4311 against 4252-4347 tok/s and 32 rows of the
+// 0.6B at U[128, 2048] 17.5-17.6k against 16.8-17.3k tok/s, where the
+// longer partitions cost more than the launch they save.
+bool step_runs_qkn(const fh_ctx* ctx, uint32_t rows) {
+  const uint32_t split = fh::attn_split_pages(rows, ctx->md.query_heads);
+  return ctx->batch_private_slots &&
+         fh::attention_qkn_supported(ctx->md.query_heads, ctx->md.kv_heads, ctx->s_qkv) &&
+         fh::attn_fuse_merge(rows, ctx->md.kv_heads, ctx->opt.context_tokens, split);
+}
+
+fh::AttnQkn step_qkn_args(fh_ctx* ctx, uint32_t l) {
+  const LayerWeights& W = ctx->layers[l];
+  return fh::AttnQkn{ctx->qkv_part,   ctx->s_qkv,     fh::kMaxRows,         W.q_norm,
+                     W.k_norm,        ctx->cos_t,     ctx->sin_t,           kv_cache(ctx, l, 0),
+                     kv_cache(ctx, l, 1), ctx->md.rms_epsilon};
+}
+
 hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   const fh_model_desc& md = ctx->md;
   const fh_ctx_options& op = ctx->opt;
@@ -415,6 +451,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   const uint32_t sq = ctx->s_qkv, so = ctx->s_o, sd = ctx->s_down;
   const uint32_t split = fh::attn_split_pages(R, QH);
   const bool fuse = fh::attn_fuse_merge(R, KVH, C, split);
+  const bool qkn = step_runs_qkn(ctx, R);
   // The step's tokens, positions and page tables come in from the pinned
   // host mirror by the first launch, so a replayed graph needs no copy beside it.
   const uint32_t meta_words = 2 * cap + R * stride;
@@ -438,13 +475,20 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
       return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part, ctx->nqkv,
                              err, s);
     });
-    L(FH_KC_QKNORM_ROPE_KV, [&] {
-      return fh::launch_qknorm_rope_kv(nullptr, ctx->qkv_part, sq, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos,
-                                       d_tab, ctx->qrot, kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon, err, s);
-    });
+    // Where no row reads another row's new slot, the attention partitions
+    // run the QK-norm/RoPE/KV append themselves (same arithmetic, bit for
+    // bit), which saves a launch per layer.
+    if (!qkn)
+      L(FH_KC_QKNORM_ROPE_KV, [&] {
+        return fh::launch_qknorm_rope_kv(nullptr, ctx->qkv_part, sq, W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t,
+                                         d_pos, d_tab, ctx->qrot, kc, vc, R, QH, KVH, stride, P, C, md.rms_epsilon,
+                                         err, s);
+      });
+    const fh::AttnQkn qa = step_qkn_args(ctx, l);
     L(FH_KC_ATTENTION, [&] {
       return fh::launch_attention_partial(ctx->qrot, kc, vc, d_pos, d_tab, ctx->attn_part, ctx->attn, 1, 0, R, R, QH,
-                                          KVH, stride, P, C, split, fuse ? ctx->attn_count : nullptr, err, s);
+                                          KVH, stride, P, C, split, fuse ? ctx->attn_count : nullptr, err, s,
+                                          qkn ? &qa : nullptr);
     });
     if (!fuse)
       L(FH_KC_ATTENTION_MERGE, [&] {
@@ -1081,7 +1125,9 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   uint64_t launches = 0;
   if (ctx->profiling) ctx->prof_launches.clear();
   if (ctx->opt.use_graphs && !ctx->profiling) {
-    auto it = ctx->graphs.find(nrows);
+    // One graph per row count and per form of the attention stage.
+    const uint32_t key = nrows | (step_runs_qkn(ctx, nrows) ? 1u << 16 : 0u);
+    auto it = ctx->graphs.find(key);
     if (it == ctx->graphs.end()) {
       hipGraph_t g = nullptr;
       hipGraphExec_t ge = nullptr;
@@ -1097,7 +1143,7 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
         return poison(FH_ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
       }
       ctx->graph_defs.push_back(g);
-      it = ctx->graphs.emplace(nrows, ge).first;
+      it = ctx->graphs.emplace(key, ge).first;
     }
     launches = ctx->step_launches;  // a replay issues what the capture recorded
     e = hipGraphLaunch(it->second, s);
@@ -1113,6 +1159,7 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   if (ctx->profiling) collect_profile(ctx);
   ctx->last_rows = nrows;
   ctx->last_batch_rows = nrows;
+  ctx->last_qkn = step_runs_qkn(ctx, nrows);
   ctx->last_logits = ctx->logits;
   ctx->last_was_prefill = false;
   const uint32_t errw = ctx->h_out[cap];
@@ -1176,10 +1223,13 @@ fh_status fh_time_attention(fh_ctx* ctx, uint32_t reps, float* avg_ms) {
     const bool fuse = fh::attn_fuse_merge(R, md.kv_heads, op.context_tokens, split);
     // The attention kernel class of the step: the partition launch (with the
     // merge when the step fuses it; the merge launch is a class of its own).
+    // A step that ran the QK-norm/KV append inside attention is timed in
+    // that form (it rewrites the same new slots with the same values).
+    const fh::AttnQkn qa = step_qkn_args(ctx, l);
     return fh::launch_attention_partial(ctx->qrot, kv_cache(ctx, l, 0), kv_cache(ctx, l, 1), d_pos, d_tab,
                                         ctx->attn_part, ctx->attn, 1, 0, R, R, md.query_heads, md.kv_heads,
                                         op.page_table_stride, op.physical_pages, op.context_tokens, split,
-                                        fuse ? ctx->attn_count : nullptr, ctx->err, s);
+                                        fuse ? ctx->attn_count : nullptr, ctx->err, s, ctx->last_qkn ? &qa : nullptr);
   };
   hipEvent_t a = nullptr, b = nullptr;
   (void)hipGetLastError();

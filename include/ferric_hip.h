@@ -290,6 +290,24 @@ fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, cons
                                 uint32_t stride, uint32_t physical_pages, uint32_t context_tokens,
                                 uint32_t* error_word, void* stream);
 
+/* K3 + K4 in one launch pair: the QK-norm + RoPE + paged KV append of fh_op_qknorm_rope_kv
+ * (same arithmetic, bit for bit) run by the attention partitions of fh_op_paged_attention.
+ * qkv_partials: qkv_splits FP32 split-K slabs of [fh_partial_slab_rows(rows)][(qh + 2*kvh) * 128]
+ * (rows <= 32); each partition forms its query heads from them, and the partition holding a
+ * row's position appends that row's K/V to the caches and uses them. The caller must not list a
+ * row's written page in another row's table (rows of one sequence in one batch read each
+ * other's new slots: run fh_op_qknorm_rope_kv then fh_op_paged_attention for those).
+ * Shapes: query_heads / kv_heads in {1, 2, 4}, qkv_splits == 2. out, out_tiled and scratch as
+ * in fh_op_paged_attention. Replaces the same reference kernels as the two calls it fuses
+ * (batched.rs:1956-1982, rope_kv.rs:102, rope_kv.rs:261, paged_decode.rs:222). */
+fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_splits, const uint16_t* q_norm,
+                                       const uint16_t* k_norm, const float* cos_table, const float* sin_table,
+                                       const uint32_t* positions, const uint32_t* page_table, uint16_t* k_cache,
+                                       uint16_t* v_cache, uint16_t* out, uint32_t out_tiled, void* scratch,
+                                       uint32_t rows, uint32_t query_heads, uint32_t kv_heads, uint32_t stride,
+                                       uint32_t physical_pages, uint32_t context_tokens, float epsilon,
+                                       uint32_t* error_word, void* stream);
+
 /* No counterpart in the reference: fh_op_paged_attention without a workspace, for
  * callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). The partition records live in a

@@ -143,6 +143,12 @@ def test_ops_reject_bad_shapes_before_any_launch():
     assert lib.fh_op_residual_rmsnorm(p, p, 2, p, p, 1, 257, 4096, 1e-6, None, None) == 1  # partials above 256 rows
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 6, 4, 4, 64, None, None) == 1  # 32 % 6
     assert lib.fh_op_paged_attention(p, p, p, p, p, p, 0, p, 1, 32, 8, 4, 4, 65, None, None) == 1  # stride*16 < ctx
+    # fused QK-norm + attention: 2 slabs, at most 4 query heads per KV head, at most 32 rows
+    qkn = lambda splits, rows, qh: lib.fh_op_qknorm_paged_attention(  # noqa: E731
+        p, splits, p, p, p, p, p, p, p, p, p, 1, p, rows, qh, 8, 64, 64, 1024, 1e-6, None, None)
+    assert qkn(3, 4, 32) == 1 and qkn(1, 4, 32) == 1  # slab count
+    assert qkn(2, 4, 64) == 1  # 8 query heads per KV head
+    assert qkn(2, 33, 32) == 1 and qkn(2, 0, 32) == 1  # rows
 
 
 def test_create_rejects_unsupported_shapes_without_touching_the_device():

@@ -515,6 +515,129 @@ def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
     assert worst <= 1e-2, worst
 
 
+# (qh, kvh, positions): 32-page partitions with the separate merge (14 rows of
+# the 8B shape, one to 17 partitions), 16-page partitions (one 8B row at a
+# 4095-token context; 0.6B rows), pages of one and of several tokens, a
+# batch of 32 rows.
+@pytest.mark.parametrize("qh,kvh,positions", [
+    (32, 8, [0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 4190, 77, 3000, 2047]),
+    (32, 8, [4095]),
+    (16, 8, [0, 17, 300, 2047, 1500, 999, 16, 4000]),
+    (32, 8, "b32"),
+    (16, 8, "b32"),
+])
+def test_qknorm_paged_attention_equals_the_two_launches(qh, kvh, positions):
+    # The decode step's fused form (QK-norm + RoPE + KV append inside the
+    # attention partitions) against fh_op_qknorm_rope_kv then
+    # fh_op_paged_attention on the same split-K slabs: attention output, K and
+    # V caches and the error word bit for bit. Each row writes a page no
+    # other row lists (the fused form's contract).
+    r = rng(4242 + qh + (len(positions) if isinstance(positions, list) else 99))
+    pages, stride, context = 4096, 264, 4224
+    if positions == "b32":
+        positions = r.integers(0, 2048, 32)
+    positions = np.asarray(positions, np.uint32)
+    rows = len(positions)
+    per_row = pages // rows
+    perm = r.permutation(pages).astype(np.uint32)
+    table = np.full((rows, stride), 0xFFFFFFFF, np.uint32)
+    for i in range(rows):
+        n = min(stride, per_row)
+        table[i, :n] = perm[i * per_row:i * per_row + n]
+        assert int(positions[i]) // 16 < n
+    ld = (qh + 2 * kvh) * 128
+    slab_rows = int(LIB.fh_partial_slab_rows(rows))
+    # Two slabs of random FP32 partial sums (their ordered sum is rounded to bf16).
+    slabs = (r.standard_normal((2, slab_rows, ld)) * 0.7).astype(np.float32)
+    qn = rand_bf16(r, 128, 1.0)
+    kn = rand_bf16(r, 128, 1.0)
+    cos = np.zeros(context * 64, np.float32)
+    sin = np.zeros(context * 64, np.float32)
+    for p in np.unique(positions):
+        c, s = orc.rope_table(int(p))
+        cos[p * 64:(p + 1) * 64], sin[p * 64:(p + 1) * 64] = c, s
+    kc0, vc0 = _paged_pool(r, pages, kvh)
+    keep = [du.to_dev(a) for a in (slabs.reshape(-1), qn, kn, cos, sin, positions, table)]
+    dslab, dqn, dkn, dcos, dsin, dpos, dtab = keep
+    scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
+    out_n = tiled_rows(rows) * qh * 128
+
+    # two launches
+    kca, vca = du.to_dev(kc0), du.to_dev(vc0)
+    q = du.empty(rows * qh * 128, np.uint16)
+    outa = du.empty(out_n, np.uint16)
+    erra = du.empty(1, np.uint32)
+    _lib.check(LIB.fh_op_qknorm_rope_kv(du.ptr(dslab), 2, du.ptr(dqn), du.ptr(dkn), du.ptr(dcos), du.ptr(dsin),
+                                        du.ptr(dpos), du.ptr(dtab), du.ptr(q), du.ptr(kca), du.ptr(vca), rows, qh,
+                                        kvh, stride, pages, context, 1e-6, du.ptr(erra), du.stream()))
+    _lib.check(LIB.fh_op_paged_attention(du.ptr(q), du.ptr(kca), du.ptr(vca), du.ptr(dpos), du.ptr(dtab),
+                                         du.ptr(outa), 1, du.ptr(scratch), rows, qh, kvh, stride, pages, context,
+                                         du.ptr(erra), du.stream()))
+    # fused
+    kcb, vcb = du.to_dev(kc0), du.to_dev(vc0)
+    outb = du.empty(out_n, np.uint16)
+    errb = du.empty(1, np.uint32)
+    scratch.zero_()
+    _lib.check(LIB.fh_op_qknorm_paged_attention(du.ptr(dslab), 2, du.ptr(dqn), du.ptr(dkn), du.ptr(dcos),
+                                                du.ptr(dsin), du.ptr(dpos), du.ptr(dtab), du.ptr(kcb), du.ptr(vcb),
+                                                du.ptr(outb), 1, du.ptr(scratch), rows, qh, kvh, stride, pages,
+                                                context, 1e-6, du.ptr(errb), du.stream()))
+    ea, eb = du.to_host(erra, np.uint32)[0], du.to_host(errb, np.uint32)[0]
+    assert ea == 0 and eb == 0, (ea, eb)
+    assert np.array_equal(du.to_host(kca, np.uint16), du.to_host(kcb, np.uint16)), "K cache"
+    assert np.array_equal(du.to_host(vca, np.uint16), du.to_host(vcb, np.uint16)), "V cache"
+    ga, gb = du.to_host(outa, np.uint16), du.to_host(outb, np.uint16)
+    assert np.array_equal(ga, gb), f"attention output: {int(np.sum(ga != gb))} of {ga.size} words differ"
+    # The appended slots hold the new token (not the pool's old contents).
+    assert not np.array_equal(du.to_host(kcb, np.uint16), kc0)
+
+
+def test_qknorm_paged_attention_errors_match_the_two_launches():
+    # A row whose written page is outside the pool, and one whose position is
+    # outside the context: the same error bits as the two-launch form
+    # (page fault; position and page fault), and no slot written for them.
+    r = rng(31)
+    qh, kvh, pages, stride, context = 32, 8, 256, 64, 1024
+    positions = np.array([100, 40, 1024, 7], np.uint32)
+    rows = len(positions)
+    table = np.full((rows, stride), 0xFFFFFFFF, np.uint32)
+    perm = r.permutation(pages).astype(np.uint32)
+    for i in range(rows):
+        table[i] = perm[i * stride:(i + 1) * stride]
+    table[1, 40 // 16] = pages + 3
+    ld = (qh + 2 * kvh) * 128
+    slabs = (r.standard_normal((2, int(LIB.fh_partial_slab_rows(rows)), ld)) * 0.7).astype(np.float32)
+    qn, kn = rand_bf16(r, 128, 1.0), rand_bf16(r, 128, 1.0)
+    cos = np.zeros(context * 64, np.float32)
+    sin = np.zeros(context * 64, np.float32)
+    kc0, vc0 = _paged_pool(r, pages, kvh)
+    keep = [du.to_dev(a) for a in (slabs.reshape(-1), qn, kn, cos, sin, positions, table)]
+    dslab, dqn, dkn, dcos, dsin, dpos, dtab = keep
+    scratch = torch.zeros(LIB.fh_attention_scratch_bytes(rows, qh, context) // 4, dtype=torch.float32, device="cuda")
+    res = []
+    for fused in (False, True):
+        kc, vc = du.to_dev(kc0), du.to_dev(vc0)
+        out = du.empty(tiled_rows(rows) * qh * 128, np.uint16)
+        err = du.empty(1, np.uint32)
+        if fused:
+            _lib.check(LIB.fh_op_qknorm_paged_attention(du.ptr(dslab), 2, du.ptr(dqn), du.ptr(dkn), du.ptr(dcos),
+                                                        du.ptr(dsin), du.ptr(dpos), du.ptr(dtab), du.ptr(kc),
+                                                        du.ptr(vc), du.ptr(out), 1, du.ptr(scratch), rows, qh, kvh,
+                                                        stride, pages, context, 1e-6, du.ptr(err), du.stream()))
+        else:
+            q = du.empty(rows * qh * 128, np.uint16)
+            _lib.check(LIB.fh_op_qknorm_rope_kv(du.ptr(dslab), 2, du.ptr(dqn), du.ptr(dkn), du.ptr(dcos),
+                                                du.ptr(dsin), du.ptr(dpos), du.ptr(dtab), du.ptr(q), du.ptr(kc),
+                                                du.ptr(vc), rows, qh, kvh, stride, pages, context, 1e-6,
+                                                du.ptr(err), du.stream()))
+            _lib.check(LIB.fh_op_paged_attention(du.ptr(q), du.ptr(kc), du.ptr(vc), du.ptr(dpos), du.ptr(dtab),
+                                                 du.ptr(out), 1, du.ptr(scratch), rows, qh, kvh, stride, pages,
+                                                 context, du.ptr(err), du.stream()))
+        res.append((du.to_host(err, np.uint32)[0], du.to_host(kc, np.uint16), du.to_host(vc, np.uint16)))
+    assert res[0][0] == res[1][0] == 4 | 8, (res[0][0], res[1][0])
+    assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+
+
 def test_paged_attention_out_of_pool_page_is_a_page_error():
     # A page-table entry past the pool is an index fault (the reference traps
     # on it, paged_decode.rs:440-470): the error word carries the page bit, not
