@@ -146,8 +146,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   constexpr bool kQkn = QKS > 0;
   static_assert(!kQkn || G + 2 <= WAVES, "one wave per query head, one for the key and one for the value head");
   // With at most two pages per wave the V registers fit beside K's, so V is
-  // requested together with K (one memory round trip instead of two).
-  constexpr bool kEarlyV = kQkn && kWavePages <= 2;
+  // requested together with K (one memory round trip instead of two). Not
+  // for G = 2 (Qwen3-0.6B), whose partitions would drop from 3 to 2
+  // workgroups per CU with the extra registers.
+  constexpr bool kEarlyV = kQkn && kWavePages <= 2 && G >= 4;
   const uint32_t split = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
   // The wave index is uniform; saying so keeps every page address scalar.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

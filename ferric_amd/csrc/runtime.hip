@@ -410,12 +410,16 @@ struct Enq {
 // 4096-token context 3.538 -> 3.467-3.483 ms per step; 32 rows of the 8B at
 // contexts U[512, 8192] 4311 against 4252-4347 tok/s and 32 rows of the
 // 0.6B at U[128, 2048] 17.5-17.6k against 16.8-17.3k tok/s, where the
-// longer partitions cost more than the launch they save.
+// longer partitions cost more than the launch they save. Models with at
+// most 2 query heads per KV head (Qwen3-0.6B) take it at any size once V is
+// requested after the scores there (occupancy kept at 3 workgroups per CU):
+// 32 rows 1.741-1.742 -> 1.733-1.734 ms device time per step.
 bool step_runs_qkn(const fh_ctx* ctx, uint32_t rows) {
   const uint32_t split = fh::attn_split_pages(rows, ctx->md.query_heads);
   return ctx->batch_private_slots &&
          fh::attention_qkn_supported(ctx->md.query_heads, ctx->md.kv_heads, ctx->s_qkv) &&
-         fh::attn_fuse_merge(rows, ctx->md.kv_heads, ctx->opt.context_tokens, split);
+         (fh::attn_fuse_merge(rows, ctx->md.kv_heads, ctx->opt.context_tokens, split) ||
+          ctx->md.query_heads <= 2 * ctx->md.kv_heads);
 }
 
 fh::AttnQkn step_qkn_args(fh_ctx* ctx, uint32_t l) {
