@@ -53,6 +53,11 @@ PREFILL_WORKLOADS = {
     "qwen3-8b-prefill": ("8b", 32, 256, "Qwen3-8B shape, one chunked-prefill batch of 32 prompts x 256 random ids "
                                         "from position 0 into a shuffled 16-token page pool; greedy first token"),
 }
+# One request end to end: (model, prompt tokens, decode steps, description)
+REQUEST_WORKLOADS = {
+    "qwen3-0.6b-b1-prompt": ("0.6b", 16, 8, "Qwen3-0.6B shape, batch 1: a 16-token prompt (ids U[0,151936)) as one "
+                                            "16-row batch, then 8 greedy decode steps, 16-token pages"),
+}
 SPEC_WORKLOADS = {
     "qwen3-8b-speculative": (32, 256, 4, "Qwen3-8B target + Qwen3-0.6B draft (random init), 32 prompts x 256 "
                                          "random ids prefilled into both, then greedy speculative rounds with K=4"),
@@ -66,10 +71,13 @@ def parse():
     p.add_argument("--steps", type=int, default=64)
     p.add_argument("--warmup", type=int, default=4)
     p.add_argument("--workload", default="qwen3-8b-b32",
-                   choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(SPEC_WORKLOADS))
+                   choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(REQUEST_WORKLOADS)
+                   + sorted(SPEC_WORKLOADS))
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-steps", type=int, default=2, help="decode steps the CPU oracle sample runs")
+    p.add_argument("--cpu-prefill-tokens", type=int, default=256,
+                   help="prompt tokens of the one sequence the prefill workload's CPU oracle sample prefills")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of HIP graph replays")
     p.add_argument("--profile-steps", type=int, default=16,
                    help="eager steps with per-launch HIP events after the timed steps (per-kernel times, roofline)")
@@ -271,7 +279,134 @@ def prefill_bench(args, name):
         "kernels": {k: {"ms_per_step": round(v, 3)} for k, v in sorted(class_ms.items(), key=lambda kv: -kv[1])},
     }
     runner.close()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = prefill_cpu_baseline(cfg, min(args.cpu_prefill_tokens, tokens), args.seed)
     print(json.dumps(result), flush=True)
+
+
+def prefill_cpu_baseline(cfg, tokens, seed):
+    """Times the CPU oracle prefilling one sequence's prompt of `tokens` ids
+    from position 0 (one forward over all its rows, every layer, FP32 head
+    and argmax for the last row)."""
+    from oracle import oracle as orc
+
+    stride = (tokens + 15) // 16
+    m = orc.Model(cfg, stride)
+    try:
+        t0 = time.perf_counter()
+        m.synthesize(seed, 0.02)
+        setup_s = time.perf_counter() - t0
+        ids = np.random.default_rng(seed).integers(0, cfg["vocabulary"], tokens)
+        table = np.full((tokens, stride), 0xFFFFFFFF, np.uint32)
+        table[:, :] = np.arange(stride, dtype=np.uint32)
+        counts = np.full(tokens, stride, np.uint32)
+        t1 = time.perf_counter()
+        m.forward(ids, np.arange(tokens), table, counts, stride, want_logits=False)
+        elapsed = time.perf_counter() - t1
+        return {
+            "value": round(tokens / elapsed, 2),
+            "unit": "tokens/s",
+            "cores": orc.threads(),
+            "kind": "port",
+            "sample": (f"one sequence's {tokens}-token prompt prefilled from position 0 ({cfg['layers']} layers, "
+                       f"every row's K/V written, FP32 head and argmax for every row) in {elapsed:.2f} s, "
+                       f"tokens/s of that sample (the GPU leg prefills 32 such prompts in one chunk); weight "
+                       f"generation {setup_s:.1f} s untimed"),
+        }
+    finally:
+        m.close()
+
+
+def request_bench(args, name):
+    """One request end to end, repeated: a prompt batch, then greedy decode
+    steps on the same sequence (a fresh sequence per request)."""
+    import torch
+
+    import ferric_amd
+    from ferric_amd import PagedLimits, PagePool, TpBatchRunner
+
+    model_key, prompt_len, decode_steps, desc = REQUEST_WORKLOADS[name]
+    cfg = dict(ferric_amd.QWEN3_8B if model_key == "8b" else ferric_amd.QWEN3_0_6B)
+    ctx = (prompt_len + decode_steps + 15) // 16 * 16
+    limits = PagedLimits(context_tokens=ctx, physical_page_count=4 * (ctx // 16), page_table_stride=ctx // 16)
+    runner = TpBatchRunner(cfg, limits, row_capacity=prompt_len, use_graphs=not args.eager)
+    runner.synthesize_weights(args.seed, 0.02)
+    pool = PagePool(limits, seed=args.seed)
+    prompt = [int(t) for t in np.random.default_rng(args.seed).integers(0, cfg["vocabulary"], prompt_len)]
+
+    def request():
+        sid = pool.admit(0)
+        b = pool.prepare([(sid, t) for t in prompt])
+        tok = runner.execute_batch(b, [prompt_len - 1]).choices[0]
+        pool.commit(b)
+        out = []
+        for _ in range(decode_steps):
+            b = pool.prepare([(sid, tok)])
+            tok = runner.execute_batch(b, [0]).choices[0]
+            pool.commit(b)
+            out.append(tok)
+        pool.release(sid)
+        return out
+
+    for _ in range(args.warmup):
+        request()
+    reqs = max(1, args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reqs):
+        tokens = request()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    result = {
+        "metric": f"decode tokens/s per request, {desc}",
+        "value": round(decode_steps * reqs / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": reqs, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / reqs, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": desc, "prompt_tokens": prompt_len, "decode_steps": decode_steps,
+                   "step": "one request: the prompt batch plus the decode steps", "graphs": not args.eager,
+                   "last_request_tokens": [int(t) for t in tokens]},
+    }
+    runner.close()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = request_cpu_baseline(cfg, prompt, decode_steps, args.seed)
+    print(json.dumps(result), flush=True)
+
+
+def request_cpu_baseline(cfg, prompt, decode_steps, seed):
+    """The CPU oracle running the same request end to end (prompt forward,
+    then the decode steps, each feeding its greedy choice to the next)."""
+    from oracle import oracle as orc
+
+    ctx = (len(prompt) + decode_steps + 15) // 16 * 16
+    stride = ctx // 16
+    m = orc.Model(cfg, stride)
+    try:
+        t0 = time.perf_counter()
+        m.synthesize(seed, 0.02)
+        setup_s = time.perf_counter() - t0
+        table = np.full((len(prompt), stride), 0xFFFFFFFF, np.uint32)
+        table[:, :] = np.arange(stride, dtype=np.uint32)
+        t1 = time.perf_counter()
+        n = len(prompt)
+        out = m.forward(prompt, np.arange(n), table, np.full(n, stride, np.uint32), stride, want_logits=False)
+        tok = int(out["choices"][-1])
+        for i in range(decode_steps):
+            out = m.forward([tok], [n + i], table[:1], np.full(1, stride, np.uint32), stride, want_logits=False)
+            tok = int(out["choices"][0])
+        elapsed = time.perf_counter() - t1
+        return {
+            "value": round(decode_steps / elapsed, 2),
+            "unit": "tokens/s",
+            "cores": orc.threads(),
+            "kind": "port",
+            "sample": (f"the same request end to end ({len(prompt)}-token prompt forward, then {decode_steps} "
+                       f"decode steps, {cfg['layers']} layers, FP32 head, argmax): {elapsed:.2f} s; weight "
+                       f"generation {setup_s:.1f} s untimed"),
+        }
+    finally:
+        m.close()
 
 
 def speculative_bench(args, name):
@@ -358,6 +493,9 @@ def main():
         return
     if args.workload in SPEC_WORKLOADS:
         speculative_bench(args, args.workload)
+        return
+    if args.workload in REQUEST_WORKLOADS:
+        request_bench(args, args.workload)
         return
 
     import torch

@@ -114,6 +114,7 @@ SIGNATURES = [
     ("fh_read_hidden", _st, [_vp, _u32, _u16p, _u64]),
     ("fh_row_capacity", _u32, [_vp]),
     ("fh_dispatch_count", _u64, [_vp]),
+    ("fh_expected_dispatch_count", _st, [_vp, _u64, ctypes.POINTER(Row), _u32, _u32p, _u32, _u64p]),
     ("fh_last_step_ms", ctypes.c_float, [_vp]),
     ("fh_set_profiling", _st, [_vp, _u32]),
     ("fh_kernel_class_ms", _st, [_vp, _u32, _f32p, _u32p]),

@@ -40,6 +40,17 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// The in-kernel merge (FUSED) publishes partition records with relaxed
+// agent-scope atomic stores, waits for them (s_waitcnt), then counts the
+// workgroup in with a relaxed atomic; the last workgroup reads the records
+// with relaxed agent-scope atomic loads. There is no release/acquire pair:
+// correctness rests on how gfx950 lowers these operations (stores written
+// through the XCD's L2 with sc1, loads that bypass it, and a wait that
+// covers store completion), so this file is built for gfx950 only.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "k_attention.hip: the in-kernel partition merge is written for gfx950's memory-model lowering"
+#endif
+
 namespace fh {
 
 namespace {

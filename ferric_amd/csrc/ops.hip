@@ -137,48 +137,48 @@ fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint1
 // ---- no-allocation attention ----------------------------------------------
 // fh_op_paged_attention_noalloc keeps its partition records in this
 // file-scope device array instead of a caller workspace. In host code
-// `scratch` is only a stand-in symbol: its device address is resolved once
-// per device (hipGetSymbolAddress, with that device current) and only that
-// address is ever handed to kernels. Every call on a GPU shares the GPU's
+// `g_noalloc_attn_records` is only a stand-in symbol: its device address is
+// resolved once per device (hipGetSymbolAddress, with that device current)
+// and only that address is ever handed to kernels. Every call on a GPU shares the GPU's
 // copy, so calls that overlap on one GPU race; each call writes every record
 // it later reads, so nothing needs clearing between calls.
 namespace {
 constexpr uint64_t kNoAllocAttnRecords = 16384;  // rows x query heads x partitions (8.5 MB)
 constexpr int kNoAllocMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_dev[kNoAllocMaxDevices] = {};
+std::mutex g_records_mu;
+void* g_records_dev[kNoAllocMaxDevices] = {};
 }  // namespace
 
-static __device__ __align__(256) float scratch[kNoAllocAttnRecords * fh::kAttnPartialFloats];
+static __device__ __align__(256) float g_noalloc_attn_records[kNoAllocAttnRecords * fh::kAttnPartialFloats];
 
 namespace {
-// The device address of `scratch` on the stream's device (NULL and an error
-// message on failure).
-float* noalloc_scratch(hipStream_t s) {
+// The device address of `g_noalloc_attn_records` on the stream's device (NULL
+// and an error message on failure).
+float* noalloc_records(hipStream_t s) {
   int dev = -1;
   hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) {
     fh::set_thread_error(e != hipSuccess ? hipGetErrorString(e) : "device ordinal out of range");
     return nullptr;
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_dev[dev]) {
+  std::lock_guard<std::mutex> lock(g_records_mu);
+  if (!g_records_dev[dev]) {
     int cur = -1;
     e = hipGetDevice(&cur);
     if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
     void* ptr = nullptr;
-    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_noalloc_attn_records));
     if (cur >= 0 && cur != dev) {
       const hipError_t r = hipSetDevice(cur);
       if (e == hipSuccess) e = r;
     }
     if (e != hipSuccess || !ptr) {
-      fh::set_thread_error(e != hipSuccess ? hipGetErrorString(e) : "no device address for the scratch array");
+      fh::set_thread_error(e != hipSuccess ? hipGetErrorString(e) : "no device address for the record array");
       return nullptr;
     }
-    g_scratch_dev[dev] = ptr;
+    g_records_dev[dev] = ptr;
   }
-  return reinterpret_cast<float*>(g_scratch_dev[dev]);
+  return reinterpret_cast<float*>(g_records_dev[dev]);
 }
 }  // namespace
 
@@ -199,11 +199,11 @@ fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cac
   const uint64_t records = (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens, split_pages);
   if (records > kNoAllocAttnRecords) {
     fh::set_thread_error("fh_op_paged_attention_noalloc: rows x query_heads x partitions of the context exceeds "
-                         "the 16384 partition records of its static scratch");
+                         "the 16384 partition records of its static array");
     return FH_ERR_INVALID_ARGUMENT;
   }
   hipStream_t s = as_stream(stream);
-  float* part = noalloc_scratch(s);
+  float* part = noalloc_records(s);
   if (!part) return FH_ERR_DEVICE;
   (void)hipGetLastError();
   hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,

@@ -3,8 +3,10 @@
 // replacement for EngineeringTpBatchExecutionV2::forward
 // (adapters/m1-engineering-execution-v1/src/tp_execution/batched.rs:1746-2454).
 //
-// One step = 4 + 9 * layers kernel launches on one HIP stream, optionally
-// replayed from a HIP graph captured once per row count. All per-step inputs
+// One decode step = 6 + (7, 8 or 9) x layers kernel launches on one HIP
+// stream (enqueue_step; fh_expected_dispatch_count counts the same code
+// without launching), optionally replayed from a HIP graph captured once per
+// row count and attention form. All per-step inputs
 // (tokens, positions, page tables) live in one device block that the step's
 // first launch refreshes from a coherent pinned host block, and the last
 // launch stores the choices and error word into another, so a captured
@@ -126,12 +128,17 @@ struct fh_ctx {
   bool poisoned = false;
   uint64_t last_batch = 0;
   uint64_t dispatches = 0;
-  uint64_t step_launches = 0;
   uint32_t last_rows = 0;        // rows with logits in the last batch (output rows for prefill)
   uint32_t last_batch_rows = 0;  // token rows of the last batch
   std::string error;
 
-  std::map<uint32_t, hipGraphExec_t> graphs;
+  // One captured decode step per row count and attention form, with the
+  // number of launches the capture recorded (what a replay issues).
+  struct StepGraph {
+    hipGraphExec_t exec = nullptr;
+    uint64_t launches = 0;
+  };
+  std::map<uint32_t, StepGraph> graphs;
   std::vector<hipGraph_t> graph_defs;
   hipEvent_t ev_begin = nullptr, ev_end = nullptr;
   float last_ms = 0.f;
@@ -369,8 +376,11 @@ fh_status validate_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uin
 }
 
 // ---- the step ---------------------------------------------------------------
+// Issues a step's launches in order, or, dry, only counts them: the dispatch
+// preflight runs the same enqueue code as the step, so the two cannot drift.
 struct Enq {
   fh_ctx* ctx;
+  bool dry = false;
   uint32_t next_event = 0;
   uint64_t launches = 0;
   hipError_t first_error = hipSuccess;
@@ -379,6 +389,10 @@ struct Enq {
 
   template <typename F>
   void run(uint32_t cls, F&& f) {
+    if (dry) {
+      ++launches;
+      return;
+    }
     const bool prof = ctx->profiling;
     hipEvent_t b = nullptr, e = nullptr;
     if (prof && next_event + 1 < ctx->prof_events.size()) {
@@ -429,7 +443,8 @@ fh::AttnQkn step_qkn_args(fh_ctx* ctx, uint32_t l) {
                      kv_cache(ctx, l, 1), ctx->md.rms_epsilon};
 }
 
-hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
+// Enqueues (or, dry, only counts) the launches of a decode step of R rows.
+hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = false) {
   const fh_model_desc& md = ctx->md;
   const fh_ctx_options& op = ctx->opt;
   hipStream_t s = ctx->stream;
@@ -440,8 +455,8 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   const uint32_t* d_pos = ctx->d_meta + cap;
   const uint32_t* d_tab = ctx->d_meta + 2 * cap;
   uint32_t* err = ctx->err;
-  Enq q{ctx};
-  (void)hipGetLastError();  // launch statuses below then belong to these launches
+  Enq q{ctx, dry};
+  if (!dry) (void)hipGetLastError();  // launch statuses below then belong to these launches
   uint64_t n = 0;
   auto L = [&](uint32_t cls, auto&& f) {
     q.run(cls, f);
@@ -531,7 +546,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches) {
   });
   ++n;  // argmax is two launches
   *launches = n;
-  ctx->step_launches = n;
+  if (dry) return hipSuccess;
   if (q.first_error != hipSuccess)
     ctx->launch_detail = std::string(" (kernel class ") + std::to_string(q.first_error_class) + ", launch " +
                          std::to_string(q.first_error_launch) + ")";
@@ -732,7 +747,7 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
 void fh_destroy(fh_ctx* ctx) {
   if (!ctx) return;
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
-  for (auto& kv : ctx->graphs) hipGraphExecDestroy(kv.second);
+  for (auto& kv : ctx->graphs) hipGraphExecDestroy(kv.second.exec);
   for (auto g : ctx->graph_defs) hipGraphDestroy(g);
   for (auto ev : ctx->prof_events) hipEventDestroy(ev);
   if (ctx->ev_begin) hipEventDestroy(ctx->ev_begin);
@@ -910,74 +925,31 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
   return FH_OK;
 }
 
-// A prefill chunk (row_capacity < nrows <= prefill_rows), launched eagerly:
-// the decode path's op order (batched.rs:1746-2454). Up to 256 rows (a
-// speculative verify) the projections are the panel GEMM with split-K
-// partials folded by the norms, as in a decode step; beyond that the
-// compute-bound 256 x 256-block kernel with the residual (and, for QKV, the
-// QK-norm, RoPE and KV append) in its epilogues. Attention runs over blocks
-// of consecutive rows of one sequence (each K/V page read once per block),
-// and the final norm + FP32 head + argmax over the requested output rows
-// only.
-fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
-                      const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
+// Enqueues (or, dry, only counts) the launches of a prefill chunk of R rows
+// with nout output rows, whose metadata (tokens, positions, output rows,
+// nblocks attention blocks, page tables) is already in pre.d_meta.
+hipError_t enqueue_prefill(fh_ctx* ctx, uint32_t R, uint32_t nout, uint32_t nblocks, uint64_t* launches,
+                           bool dry = false) {
   const fh_model_desc& md = ctx->md;
   const fh_ctx_options& op = ctx->opt;
   auto& p = ctx->pre;
   const uint32_t P = op.prefill_rows, stride = op.page_table_stride;
   const uint32_t H = md.hidden, QH = md.query_heads, KVH = md.kv_heads, Q = QH * 128, I = md.intermediate,
                  V = md.vocabulary, C = op.context_tokens, pages = op.physical_pages;
-  uint32_t* tok = p.h_meta;
-  uint32_t* pos = p.h_meta + P;
-  uint32_t* outs = p.h_meta + 2 * P;
-  uint32_t* blocks = p.h_meta + 2 * P + kMaxPrefillOutputs;
-  uint32_t* tab = p.h_meta + 3 * P + kMaxPrefillOutputs;
-  for (uint32_t i = 0; i < nrows; ++i) {
-    tok[i] = rows[i].token;
-    pos[i] = rows[i].position;
-    uint32_t* t = tab + (uint64_t)i * stride;
-    std::memcpy(t, rows[i].pages, rows[i].page_count * 4);
-    std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
-  }
-  for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
-  // Attention blocks: runs of rows of one sequence at consecutive positions
-  // whose page lists extend one another (so the block's last row's table
-  // serves every row of it), at most attention_block_rows() rows each.
-  const uint32_t bq = fh::attention_block_rows(QH, KVH);
-  uint32_t nblocks = 0;
-  for (uint32_t i = 0; i < nrows;) {
-    uint32_t j = i + 1;
-    while (j < nrows && j - i < bq && rows[j].sequence == rows[i].sequence &&
-           rows[j].position == rows[j - 1].position + 1 && rows[j].page_count >= rows[j - 1].page_count &&
-           std::memcmp(rows[j].pages, rows[j - 1].pages, (size_t)rows[j - 1].page_count * 4) == 0)
-      ++j;
-    blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
-    i = j;
-  }
-  auto poison = [&](fh_status s2, const std::string& msg) {
-    ctx->poisoned = true;
-    return fail(ctx, s2, msg);
-  };
   hipStream_t s = ctx->stream;
   const uint32_t* d_tok = p.d_meta;
   const uint32_t* d_pos = p.d_meta + P;
   const uint32_t* d_out = p.d_meta + 2 * P;
   const uint32_t* d_blocks = p.d_meta + 2 * P + kMaxPrefillOutputs;
   const uint32_t* d_tab = p.d_meta + 3 * P + kMaxPrefillOutputs;
-  const uint64_t meta_bytes = (3ull * P + kMaxPrefillOutputs + (uint64_t)nrows * stride) * 4;
-  hipError_t e = hipMemcpyAsync(p.d_meta, p.h_meta, meta_bytes, hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("metadata upload: ") + hipGetErrorString(e));
-  hipEventRecord(ctx->ev_begin, s);
-  if (ctx->profiling) ctx->prof_launches.clear();
-  Enq q{ctx};
-  (void)hipGetLastError();
+  Enq q{ctx, dry};
+  if (!dry) (void)hipGetLastError();
   uint32_t* err = ctx->err;
   uint64_t n = 0;
   auto L = [&](uint32_t cls, auto&& f) {
     q.run(cls, f);
     ++n;
   };
-  const uint32_t R = nrows;
   // The fused QKV epilogue needs the 256 x 256-block projection kernel.
   const bool fused_qkv = R > 256 && ctx->nqkv % 256 == 0 && fh::act_mtiles(R) % 16 == 0;
   // Chunks of up to kPanelRows rows (a speculative verify) write split-K
@@ -1072,11 +1044,70 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     L(FH_KC_ARGMAX, [&] { return fh::launch_argmax(p.logits, nout, V, p.argmax_scratch, p.choices, err, s); });
     ++n;  // argmax is two launches
   }
-  e = q.first_error;
-  if (e != hipSuccess)
-    return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + " (kernel class " +
-                                     std::to_string(q.first_error_class) + ", launch " +
-                                     std::to_string(q.first_error_launch) + ")");
+  *launches = n;
+  if (!dry && q.first_error != hipSuccess)
+    ctx->launch_detail = std::string(" (kernel class ") + std::to_string(q.first_error_class) + ", launch " +
+                         std::to_string(q.first_error_launch) + ")";
+  return dry ? hipSuccess : q.first_error;
+}
+
+// A prefill chunk (row_capacity < nrows <= prefill_rows), launched eagerly:
+// the decode path's op order (batched.rs:1746-2454). Up to 256 rows (a
+// speculative verify) the projections are the panel GEMM with split-K
+// partials folded by the norms, as in a decode step; beyond that the
+// compute-bound 256 x 256-block kernel with the residual (and, for QKV, the
+// QK-norm, RoPE and KV append) in its epilogues. Attention runs over blocks
+// of consecutive rows of one sequence (each K/V page read once per block),
+// and the final norm + FP32 head + argmax over the requested output rows
+// only.
+fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                      const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
+  const fh_model_desc& md = ctx->md;
+  const fh_ctx_options& op = ctx->opt;
+  auto& p = ctx->pre;
+  const uint32_t P = op.prefill_rows, stride = op.page_table_stride;
+  const uint32_t QH = md.query_heads, KVH = md.kv_heads, V = md.vocabulary;
+  uint32_t* tok = p.h_meta;
+  uint32_t* pos = p.h_meta + P;
+  uint32_t* outs = p.h_meta + 2 * P;
+  uint32_t* blocks = p.h_meta + 2 * P + kMaxPrefillOutputs;
+  uint32_t* tab = p.h_meta + 3 * P + kMaxPrefillOutputs;
+  for (uint32_t i = 0; i < nrows; ++i) {
+    tok[i] = rows[i].token;
+    pos[i] = rows[i].position;
+    uint32_t* t = tab + (uint64_t)i * stride;
+    std::memcpy(t, rows[i].pages, rows[i].page_count * 4);
+    std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
+  }
+  for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
+  // Attention blocks: runs of rows of one sequence at consecutive positions
+  // whose page lists extend one another (so the block's last row's table
+  // serves every row of it), at most attention_block_rows() rows each.
+  const uint32_t bq = fh::attention_block_rows(QH, KVH);
+  uint32_t nblocks = 0;
+  for (uint32_t i = 0; i < nrows;) {
+    uint32_t j = i + 1;
+    while (j < nrows && j - i < bq && rows[j].sequence == rows[i].sequence &&
+           rows[j].position == rows[j - 1].position + 1 && rows[j].page_count >= rows[j - 1].page_count &&
+           std::memcmp(rows[j].pages, rows[j - 1].pages, (size_t)rows[j - 1].page_count * 4) == 0)
+      ++j;
+    blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
+    i = j;
+  }
+  auto poison = [&](fh_status s2, const std::string& msg) {
+    ctx->poisoned = true;
+    return fail(ctx, s2, msg);
+  };
+  hipStream_t s = ctx->stream;
+  uint32_t* err = ctx->err;
+  const uint64_t meta_bytes = (3ull * P + kMaxPrefillOutputs + (uint64_t)nrows * stride) * 4;
+  hipError_t e = hipMemcpyAsync(p.d_meta, p.h_meta, meta_bytes, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("metadata upload: ") + hipGetErrorString(e));
+  hipEventRecord(ctx->ev_begin, s);
+  if (ctx->profiling) ctx->prof_launches.clear();
+  uint64_t n = 0;
+  e = enqueue_prefill(ctx, nrows, nout, nblocks, &n);
+  if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + ctx->launch_detail);
   hipEventRecord(ctx->ev_end, s);
   if (nout) e = hipMemcpyAsync(p.h_out, p.choices, nout * 4, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipMemcpyAsync(p.h_out + kMaxPrefillOutputs, err, 4, hipMemcpyDeviceToHost, s);
@@ -1147,10 +1178,10 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
         return poison(FH_ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
       }
       ctx->graph_defs.push_back(g);
-      it = ctx->graphs.emplace(key, ge).first;
+      it = ctx->graphs.emplace(key, fh_ctx::StepGraph{ge, launches}).first;
     }
-    launches = ctx->step_launches;  // a replay issues what the capture recorded
-    e = hipGraphLaunch(it->second, s);
+    launches = it->second.launches;  // a replay issues what its capture recorded
+    e = hipGraphLaunch(it->second.exec, s);
   } else {
     e = enqueue_step(ctx, nrows, &launches);
   }
@@ -1191,6 +1222,24 @@ fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t el
     return fail(ctx, FH_ERR_INVALID_ARGUMENT, "bad hidden-state request (capture_hidden off?)");
   FH_HIP(ctx, hipMemcpy(out, ctx->capture + (uint64_t)layer * ctx->capture_rows * ctx->md.hidden, elements * 2,
                         hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+fh_status fh_expected_dispatch_count(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                                     const uint32_t* output_rows, uint32_t nout, uint64_t* count) {
+  if (!ctx || !count) return FH_ERR_INVALID_ARGUMENT;
+  if (nout && !output_rows) return fail(ctx, FH_ERR_INVALID_ARGUMENT, "null output rows");
+  // The batch is checked as fh_execute_batch checks it (which also decides
+  // whether its rows' written slots are private, one input of the policy),
+  // then the step's own enqueue code runs without launching anything.
+  fh_status st = validate_batch(ctx, batch_id, rows, nrows, output_rows, nout);
+  if (st != FH_OK) return st;
+  uint64_t n = 0;
+  if (nrows > ctx->opt.row_capacity)
+    enqueue_prefill(ctx, nrows, nout, 0, &n, true);
+  else
+    enqueue_step(ctx, nrows, &n, true);
+  *count = n;
   return FH_OK;
 }
 

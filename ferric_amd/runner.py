@@ -4,7 +4,8 @@
 `EngineeringTpBatchRunnerV2` (adapters/m1-engineering-execution-v1/src/
 tp_batch_runtime.rs:20-95): `row_capacity`, `execute_batch(batch,
 output_rows) -> BatchOutput{choices}`, `output_head_rows`,
-`expected_dispatch_counts`, `dispatch_counts`, `close`. The prepared-batch
+`expected_dispatch_counts_for_selection` / `_for_batch`, `dispatch_counts`,
+`close`. The prepared-batch
 types mirror `EngineeringTpPreparedRowV1` / `EngineeringTpPreparedBatchV1`
 (tp_paged.rs:257-350). All GPU work and all batch validation happen in
 libferric_hip.so behind the C ABI; this module only marshals.
@@ -218,8 +219,32 @@ class TpBatchRunner:
     def output_head_rows(self, physical: int, published: int) -> int:
         return physical
 
+    def expected_dispatch_counts_for_selection(self, batch: PreparedBatch, output_rows: Sequence[int]) -> list:
+        """The dispatch_counts() increment execute_batch(batch, output_rows) will
+        make (one entry: one context stands in for every rank), evaluated by
+        the library without launching (fh_expected_dispatch_count). Raises the
+        execute_batch error for a batch it would reject."""
+        if batch.limits != self.limits:
+            raise FerricError(2, "foreign, stale, or invalid prepared GPU batch")
+        rows, keep = _rows_to_c(batch.rows)
+        outs = np.ascontiguousarray(np.asarray(output_rows, dtype=np.uint32))
+        count = ctypes.c_uint64()
+        st = self._lib.fh_expected_dispatch_count(self._ctx, batch.id, rows, len(batch.rows),
+                                                  outs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(outs),
+                                                  ctypes.byref(count))
+        del keep
+        check(st, self._ctx)
+        return [int(count.value)]
+
+    def expected_dispatch_counts_for_batch(self, batch: PreparedBatch, published: int) -> list:
+        """As the reference's default: the selection of the first `published` rows."""
+        return self.expected_dispatch_counts_for_selection(batch, range(published))
+
     def expected_dispatch_counts(self, published: int) -> list:
-        return [6 + 9 * self.model["layers"]]
+        """The batch-independent form has no exact answer here: the launch
+        schedule depends on the batch (rows, written slots, prefill or decode).
+        Use expected_dispatch_counts_for_selection."""
+        raise FerricError(1, "the dispatch count depends on the batch; use expected_dispatch_counts_for_selection")
 
     def dispatch_counts(self) -> list:
         return [int(self._lib.fh_dispatch_count(self._ctx))]

@@ -129,6 +129,28 @@ def compact_completion(choices, draft, active_lengths, slots, generations, epoch
     return [bytes(out[i * 120:(i + 1) * 120]) for i in range(s)]
 
 
+# Limits of the 120-byte completion record (logits.rs:279): at most 32
+# request slots, 16 draft tokens (17 emitted), token ids below 151936.
+RECORD_MAX_SEQUENCES = 32
+RECORD_MAX_K = 16
+RECORD_VOCABULARY = 151936
+
+
+def round_records(choices, draft, k, epoch, plan):
+    """The completion records of a settled round (slot = sequence index,
+    generation 1, epoch = round), or None where the round is outside what a
+    record can hold (more than 32 sequences, K > 16, or a token id a record
+    rejects); the round itself is unaffected."""
+    choices, draft = np.asarray(choices), np.asarray(draft)
+    n = int(choices.shape[0])
+    if n == 0 or n > RECORD_MAX_SEQUENCES or k > RECORD_MAX_K:
+        return None
+    if int(choices.max()) >= RECORD_VOCABULARY or (draft.size and int(draft.max()) >= RECORD_VOCABULARY):
+        return None
+    return compact_completion(choices, draft, [k + 1] * n, list(range(n)), [1] * n, [epoch] * n, [plan] * n, k + 1,
+                              k)
+
+
 class SpeculativeDecoder:
     """Greedy speculation of a draft runner for a target runner, each with
     its own KV pool. Sequences share prompts and cursors across the two."""
@@ -193,14 +215,6 @@ class SpeculativeDecoder:
         batch = self.tpool.prepare(rows)
         choices = np.asarray(self.target.execute_batch(batch, list(range(len(rows)))).choices,
                              dtype=np.uint32).reshape(len(seqs), k + 1)
-        # Completion records (slot = sequence index, generation 1, epoch = round),
-        # for at most the 32 request slots a record can name.
-        records = None
-        if len(seqs) <= 32:
-            n = len(seqs)
-            records = compact_completion(choices, draft, [k + 1] * n, list(range(n)), [1] * n, [self.epoch] * n,
-                                         [self.plan] * n, k + 1, k)
-        self.epoch += 1
         accepted, emitted = [], []
         acc, ems = verify_greedy_batch(draft, choices)
         for j, s in enumerate(seqs):
@@ -216,4 +230,8 @@ class SpeculativeDecoder:
             s.emitted += em
             accepted.append(a)
             emitted.append(em)
+        # Completion records, built once both pools are settled (so a round
+        # whose shape a record cannot hold still leaves every cursor in step).
+        records = round_records(choices, draft, k, self.epoch, self.plan)
+        self.epoch += 1
         return RoundStats(accepted, emitted, k, len(late), len(rows), records, draft, choices)

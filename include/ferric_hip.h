@@ -169,6 +169,17 @@ fh_status fh_read_hidden(fh_ctx* ctx, uint32_t layer, uint16_t* out, uint64_t el
 uint32_t fh_row_capacity(const fh_ctx* ctx);
 /* Kernel launches issued by successful batches (dispatch_counts(), tp_batch_runtime.rs:89). */
 uint64_t fh_dispatch_count(const fh_ctx* ctx);
+/* Preflight: the increment of fh_dispatch_count that fh_execute_batch with the same arguments
+ * will make, evaluated without launching anything (the step's own enqueue code, run dry). The
+ * batch is validated first, with fh_execute_batch's error classes. The count depends on the
+ * batch: decode steps take 7, 8 or 9 launches per layer (the QK-norm/KV append runs inside the
+ * attention partitions when no row reads another row's new slot and the shape allows it; the
+ * partition merge runs in the same launch for small launches), prefill chunks another schedule,
+ * and capture_hidden adds copies. Replaces expected_dispatch_counts_for_selection
+ * (tp_batch_runtime.rs:80-86; the reference's per-batch policy is tp_execution/batched.rs:1494-1560),
+ * whose result the caller compares with the dispatch_counts() increment (tp_batch_runtime.rs:432-446). */
+fh_status fh_expected_dispatch_count(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
+                                     const uint32_t* output_rows, uint32_t nout, uint64_t* count);
 /* Device milliseconds of the last fh_execute_batch, from HIP events on the context stream. */
 float fh_last_step_ms(const fh_ctx* ctx);
 /* Per-kernel-class device time of the last batch when profiling is on (parity/bench aid).
@@ -311,9 +322,11 @@ fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_s
 /* No counterpart in the reference: fh_op_paged_attention without a workspace, for
  * callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). The partition records live in a
- * static device array of the library, 16384 records (rows x query_heads x
- * ceil(context_tokens / 512)) = 8.5 MB, held on every GPU the entry point has run
- * on until the process ends; larger launches return FH_ERR_INVALID_ARGUMENT.
+ * static device array of the library: 16384 records = 8.5 MB, held on every GPU the
+ * library has launched on until the process ends. A launch needs rows x query_heads x
+ * ceil(context_tokens / (16 x split_pages)) records, where split_pages is 16 (256-token
+ * partitions) when rows x query_heads <= 64 or query_heads <= 16, else 32 (512-token
+ * partitions); larger launches return FH_ERR_INVALID_ARGUMENT.
  * Calls that overlap on one GPU share that array and race. Same kernels and results
  * as fh_op_paged_attention. */
 fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,

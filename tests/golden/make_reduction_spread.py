@@ -102,7 +102,8 @@ def run_case(name):
             "serial_logits_sha256": hashlib.sha256(np.ascontiguousarray(ref["logits"]).tobytes()).hexdigest(),
             "serial_choices": [int(c) for c in ref["choices"]],
             "serial_gaps": [float(g) for g in ref["gaps"]],
-            "wave_vs_serial": {k: wave[k] for k in ("logit_max", "logit_rms", "drift_max", "drift", "flips")},
+            "wave_vs_serial": {k: wave[k] for k in ("logit_max", "logit_rms", "drift_max", "drift", "flips",
+                                                    "row_logit_max")},
         }
         if planted is not None:
             entry["planted_vs_serial"] = {k: planted[k] for k in ("logit_max", "logit_rms", "drift_max", "flips")}

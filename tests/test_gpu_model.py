@@ -379,11 +379,18 @@ def _decode_steps(case_name, steps, rows=32, wave_model=True):
         raise
 
 
-def test_qwen3_8b_full_depth_batch32_decode_step():
+@pytest.mark.timeout(900)
+def test_qwen3_8b_full_depth_batch32_decode_steps():
     # The decode benchmark's shape at full size (the north-star workload):
     # Qwen3-8B with all 36 layers, batch 32, contexts U[512, 8192] on 16-token
-    # pages, through the HIP-graph path.
-    _decode_steps("qwen3-8b-b32", 1, wave_model=False).close()
+    # pages, through the HIP-graph path: 3 teacher-forced steps, so KV that one
+    # step writes is read by the next, every bar at every step, and the
+    # written KV slots of the first, middle and last layer checked afterwards.
+    pair = _decode_steps("qwen3-8b-b32", 3)
+    try:
+        pair.check_kv(layer_list=[0, 17, 35])
+    finally:
+        pair.close()
 
 
 def test_qwen3_8b_batch1_context4096_decode_steps():
@@ -695,7 +702,11 @@ class ParityRunner:
             for i, ch in enumerate(out.choices):
                 want, gap = int(ref["choices"][outs[i]]), float(ref["gaps"][outs[i]])
                 if ch != want:
-                    assert int(wave_c[i]) != want or gap < max(sp.NEAR_TIE, spread), (label, i, ch, want, gap)
+                    # explained by the wave order's own logit difference on this row
+                    row_spread = float(np.max(np.abs(wave_l[i] - ref_l[i])))
+                    print(f"{label}: flip on output row {i} at gap {gap:.3e}; wave order's difference on the row "
+                          f"{row_spread:.3e}")
+                    assert int(wave_c[i]) != want or gap < max(sp.NEAR_TIE, row_spread), (label, i, ch, want, gap)
                     self.flips.append((label, i, gap))
             self.last_ref = {"choices": [int(x) for x in ref["choices"][outs]]}
         return out
@@ -771,6 +782,14 @@ def _golden_spread(case_name="qwen3-8b-b32"):
     full-depth case (tests/golden/reduction_spread.json)."""
     g = json.loads(GOLDEN_SPREAD.read_text())[case_name]["steps"][0]["wave_vs_serial"]
     return g["logit_max"], g["drift_max"]
+
+
+def _golden_row_spread(case_name="qwen3-8b-b32"):
+    """A typical row's share of that spread: the median over the case's rows
+    of the wave order's largest logit difference on the row (the per-row bar
+    for comparisons that have no oracle run of their own rows)."""
+    g = json.loads(GOLDEN_SPREAD.read_text())[case_name]["steps"][0]["wave_vs_serial"]
+    return float(np.median(g["row_logit_max"]))
 
 
 def test_prefill_8b_full_depth_two_prompts_match_oracle():
@@ -851,7 +870,7 @@ def test_prefill_32x256_full_size_kv_indexing_and_first_tokens():
             if first_pre[i] != first_dec[i]:
                 row = np.sort(logits_dec[i])
                 gap = float(row[-1] - row[-2])
-                assert gap < spread_logit, (i, first_pre[i], first_dec[i], gap)
+                assert gap < max(sp.NEAR_TIE, _golden_row_spread()), (i, first_pre[i], first_dec[i], gap)
                 print(f"sequence {i}: near-tie between the paths (gap {gap:.2e})")
         e2e = float(np.max(np.abs(logits_pre - logits_dec)))
         print(f"prefill vs decode: logits max diff {e2e:.3e} (oracle orders' spread {spread_logit:.3e})")
@@ -915,12 +934,13 @@ def test_speculative_config5_shapes_emit_the_target_greedy_stream():
             for i in range(S):
                 ref[i].append(out[i])
                 gaps[i].append(float(np.diff(np.sort(lg[i])[-2:])[0]))
-        spread_logit, _ = _golden_spread()
+        row_spread = _golden_row_spread()
         for j, s in enumerate(dec.seqs):
             for i, (got, want) in enumerate(zip(s.emitted, ref[j])):
                 if got != want:
-                    assert gaps[j][i] < spread_logit, (j, i, got, want, gaps[j][i])
-                    print(f"sequence {j}: near-tie at token {i} (gap {gaps[j][i]:.2e}); compared up to there")
+                    print(f"sequence {j}: differs at token {i} at gap {gaps[j][i]:.2e} (a typical row's oracle-order "
+                          f"spread {row_spread:.2e}); compared up to there")
+                    assert gaps[j][i] < max(sp.NEAR_TIE, row_spread), (j, i, got, want, gaps[j][i])
                     break
     finally:
         for r in (target, draft, plain):

@@ -10,7 +10,9 @@ import pytest
 
 from ferric_amd import PagedLimits, PagePool
 from ferric_amd.runner import BatchOutput
-from ferric_amd.speculative import SpeculativeDecoder, token_assembly, verify_greedy
+from ferric_amd import FerricError
+from ferric_amd.speculative import (SpeculativeDecoder, compact_completion, token_assembly, verify_greedy,
+                                      verify_greedy_batch)
 
 VOCAB = 50
 
@@ -148,3 +150,32 @@ def test_rounds_carry_compact_completion_records():
             assert rec[48] == a and rec[49] == a + 1 == len(st.emitted[s])
             assert list(struct.unpack_from(f"<{a + 1}I", rec, 52)) == st.emitted[s]
             assert rec[52 + 4 * (a + 1):] == bytes(120 - 52 - 4 * (a + 1))
+
+
+def test_rounds_wider_than_a_record_settle_without_records():
+    # K = 17 is past what a completion record holds (16 drafts, 17 emitted
+    # tokens): the record builder rejects it, while the round itself, its
+    # settlement and both pools' cursors are unaffected.
+    k = 17
+    draft = np.arange(k * 2, dtype=np.uint32).reshape(k, 2) % VOCAB
+    target = np.zeros((2, k + 1), dtype=np.uint32)
+    target[0, :] = np.append(draft[:, 0], 7)  # all accepted
+    target[1, 0] = (draft[0, 1] + 1) % VOCAB  # first rejected
+    acc, em = verify_greedy_batch(draft, target)
+    assert acc.tolist() == [k, 0]
+    assert em[0].tolist() == list(draft[:, 0]) + [7] and em[1, 0] == target[1, 0]
+    with pytest.raises(FerricError) as e:
+        compact_completion(target, draft, [k + 1] * 2, [0, 1], [1, 1], [0, 0], [bytes(range(32))] * 2, k + 1, k)
+    assert e.value.status == 1
+    dec, tgt, drf = make(k, 1000)  # the draft always agrees: every round accepts all 17
+    prompts = [[1, 2, 3], [4, 5]]
+    dec.prefill(prompts)
+    for _ in range(3):
+        st = dec.round()
+        assert st.records is None
+        assert st.accepted == [k, k]
+    for j, p in enumerate(prompts):
+        s = dec.seqs[j]
+        assert s.emitted == plain_greedy(p, len(s.emitted) - 1, 12345)
+        assert dec.tpool.sequences[s.target_sid].length == s.cursor
+        assert dec.dpool.sequences[s.draft_sid].length == s.cursor - 1  # the catch-up candidate is pending
