@@ -120,14 +120,19 @@ def kernel_bytes(cfg, rows, positions, stride):
     parts = (ctx + tokens - 1) // tokens
     merge_read = int(np.sum(np.where(parts > 1, parts, 0))) * QH * 130 * 4
     merged_rows = int(np.sum(parts > 1))
+    norm = rows * H * 2 * 2 + H * 2  # residual row in and out, norm weight
+    # One-row steps run each norm inside the projection that consumes it
+    # (QKV, gate/up, LM head), which then reads the residual row and norm
+    # weight and writes the folded row instead of reading a normalized one.
+    in_proj = norm - rows * H * 2 if rows == 1 else 0
     return {
         "attention": kv_read + rows * Q * 2,
-        "qkv_gemm": nqkv * H * 2 + rows * H * 2 + rows * nqkv * 2,
+        "qkv_gemm": nqkv * H * 2 + rows * H * 2 + rows * nqkv * 2 + in_proj,
         "o_gemm": H * Q * 2 + rows * Q * 2 + rows * H * 2 * 2,
-        "gate_up_gemm": 2 * I * H * 2 + rows * H * 2 + rows * I * 2,
+        "gate_up_gemm": 2 * I * H * 2 + rows * H * 2 + rows * I * 2 + in_proj,
         "down_gemm": H * I * 2 + rows * I * 2 + rows * H * 2 * 2,
-        "head_gemm": V * H * 2 + rows * H * 2 + rows * V * 4,
-        "rmsnorm": rows * H * 2 * 2 + H * 2,
+        "head_gemm": V * H * 2 + rows * H * 2 + rows * V * 4 + in_proj,
+        "rmsnorm": 0 if rows == 1 else norm,
         "qknorm_rope_kv": rows * nqkv * 2 + rows * Q * 2 + rows * 2 * KV * 2,
         "attention_merge": merge_read + merged_rows * Q * 2,
         "argmax": rows * V * 4,

@@ -131,6 +131,9 @@ SIGNATURES = [
     ("fh_op_tile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_untile_activation", _st, [_vp, _vp, _u32, _u32, _vp]),
     ("fh_op_residual_rmsnorm", _st, [_vp, _vp, _u32, _vp, _vp, _u32, _u32, _u32, ctypes.c_float, _vp, _vp]),
+    ("fh_op_gemm_rmsnorm", _st,
+     [_vp, _vp, _vp, _u32, _vp, ctypes.c_float, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, _vp]),
+    ("fh_gemm_rmsnorm_supported", _u32, [_u32, _u32, _u32, _u32, _u32]),
     ("fh_op_qknorm_rope_kv", _st, [_vp, _u32] + [_vp] * 9 + [_u32] * 6 + [ctypes.c_float, _vp, _vp]),
     ("fh_attention_scratch_bytes", _u64, [_u32, _u32, _u32]),
     ("fh_op_paged_attention", _st, [_vp] * 6 + [_u32, _vp] + [_u32] * 6 + [_vp, _vp]),

@@ -42,14 +42,30 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+constexpr int kRowNormThreads = 256;  // the residual + RMSNorm kernel's thread count and mapping
+
 // Batches of more than 32 rows run as 32-row chunks (gridDim.z of them, one
 // split): every chunk streams the same weight tiles.
-template <int NT, int MT, int EPI, int WAVES, int UNROLL>
+//
+// NS >= 0 (one row): the row's residual + RMSNorm runs in the prologue of
+// every workgroup (RowNormArgs; NS split-K slabs folded, NJ 16-byte chunks
+// per thread), with the norm kernel's thread mapping and reduction order
+// (threads 0..255: chunks t, t + 256, ...; squares summed per thread in chunk
+// order, then the four wave totals in wave order), so x is bit-identical to
+// that kernel's. The prologue's loads go out first and the first weight
+// chunk's right after them, so the weights stream while the row is folded
+// and reduced; x is staged in LDS and each k-block's B operand is read from
+// there (lanes 0, 16, 32, 48 hold row 0; the other 15 rows of the tile are
+// zero: they only produce the discarded output rows).
+template <int NT, int MT, int EPI, int WAVES, int UNROLL, int NS = -1, int NJ = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __restrict__ xt,
                                                          const uint16_t* __restrict__ w, uint32_t m_total,
                                                          uint32_t kb_count, uint32_t kb_split, uint32_t x_mtiles,
                                                          const uint16_t* residual, void* out, uint32_t ldo,
-                                                         uint32_t* err) {
+                                                         uint32_t* err, RowNormArgs na) {
+  constexpr bool kNorm = NS >= 0;
+  static_assert(!kNorm || MT == 1, "the fused norm serves one row");
+  static_assert(!kNorm || WAVES * 64 >= kRowNormThreads, "the norm's 256-thread mapping");
   __shared__ float red[WAVES][NT * MT * 256];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // A launch over several 32-row chunks (always one split) reads each weight
@@ -111,6 +127,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
   // scheduling barriers keep the compiler from sinking them back next to
   // their uses (which would leave one or two loads in flight per wave).
   u32x4 wa[UNROLL][NT], xa[UNROLL][MT], wb[UNROLL][NT], xb[UNROLL][MT];
+  // Fused norm: the normalized row in LDS, 8 bf16 per entry (k / 8 entries).
+  __shared__ __attribute__((aligned(16))) u32x4 xs[kNorm ? NJ * kRowNormThreads : 1];
+  __shared__ float nred[kRowNormThreads / 64];
+  // B operand of k-block kb_lo + sk from the staged row.
+  auto norm_x = [&](uint32_t sk) {
+    const u32x4 v = xs[(kb_lo + sk) * 4 + (lane >> 4)];
+    return (lane & 15) == 0 ? v : u32x4{0u, 0u, 0u, 0u};
+  };
   auto load = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT], uint32_t s0) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
@@ -118,8 +142,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
       if (sk >= whole) sk -= whole;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) wv[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)sk * 64);
+      if constexpr (kNorm) {
+        xv[u][0] = norm_x(sk);
+      } else {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)sk * xkb + mt * 64];
+        for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xp[(uint64_t)sk * xkb + mt * 64];
+      }
     }
   };
   auto compute = [&](u32x4(&wv)[UNROLL][NT], u32x4(&xv)[UNROLL][MT]) {
@@ -131,7 +159,121 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
         for (int mt = 0; mt < MT; ++mt)
           acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_b8(wv[u][nt]), as_b8(xv[u][mt]), acc[nt][mt], 0, 0, 0);
   };
-  if (chunks > 0) load(wa, xa, 0);
+  if constexpr (kNorm) {
+    // Prologue loads (norm weight, residual row, slabs), then the first
+    // weight chunk, then the fold and the reduction.
+    const int t = threadIdx.x;
+    const uint32_t width = kb_count * 32, nchunks = width / 8;
+    const uint64_t slab = (uint64_t)na.slab_rows * width;
+    uint4 hv[NJ], wv8[NJ];
+    float4 pv[NJ][NS > 0 ? NS : 1][2];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t c = t + j * kRowNormThreads;
+      if (t < kRowNormThreads && c < nchunks) wv8[j] = *reinterpret_cast<const uint4*>(na.w + c * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t c = t + j * kRowNormThreads;
+      if (t < kRowNormThreads && c < nchunks) {
+        hv[j] = *reinterpret_cast<const uint4*>(na.hidden_in + c * 8);
+        if constexpr (NS > 0) {
+          const float4* pr = reinterpret_cast<const float4*>(na.part + c * 8);
+#pragma unroll
+          for (int sp = 0; sp < NS; ++sp) {
+            pv[j][sp][0] = pr[sp * (slab / 4)];
+            pv[j][sp][1] = pr[sp * (slab / 4) + 1];
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (chunks > 0) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        uint32_t sk = u + rot;
+        if (sk >= whole) sk -= whole;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wa[u][nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)sk * 64);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float sum = 0.f;
+    bool bad = false;
+    const bool writer = NS > 0 && blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t c = t + j * kRowNormThreads;
+      if (t < kRowNormThreads && c < nchunks) {
+        if constexpr (NS > 0) {
+          // h = bf16((0 + (P_0 + P_1 + ...)) + h), the slabs in split order.
+          float a[8] = {pv[j][0][0].x, pv[j][0][0].y, pv[j][0][0].z, pv[j][0][0].w,
+                        pv[j][0][1].x, pv[j][0][1].y, pv[j][0][1].z, pv[j][0][1].w};
+#pragma unroll
+          for (int sp = 1; sp < NS; ++sp) {
+            a[0] += pv[j][sp][0].x; a[1] += pv[j][sp][0].y; a[2] += pv[j][sp][0].z; a[3] += pv[j][sp][0].w;
+            a[4] += pv[j][sp][1].x; a[5] += pv[j][sp][1].y; a[6] += pv[j][sp][1].z; a[7] += pv[j][sp][1].w;
+          }
+          uint32_t words[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = f32_to_bf16((0.0f + a[2 * q]) + lo_bf16(words[q]));
+            const uint32_t hi = f32_to_bf16((0.0f + a[2 * q + 1]) + hi_bf16(words[q]));
+            words[q] = lo | (hi << 16);
+          }
+          hv[j] = make_uint4(words[0], words[1], words[2], words[3]);
+          if (writer) *reinterpret_cast<uint4*>(na.hidden_out + c * 8) = hv[j];
+        }
+        const uint32_t words[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x0 = lo_bf16(words[q]), x1 = hi_bf16(words[q]);
+          bad |= !is_finite_f32(x0) | !is_finite_f32(x1);
+          sum = sum + x0 * x0;
+          sum = sum + x1 * x1;
+        }
+      }
+    }
+    // The four wave totals of threads 0..255, in wave order.
+    sum = wave_sum(sum);
+    if (lane == 0 && t < kRowNormThreads) nred[t >> 6] = sum;
+    __syncthreads();
+    float total = nred[0];
+#pragma unroll
+    for (int q = 1; q < kRowNormThreads / 64; ++q) total += nred[q];
+    const float inv = inverse_rms(total, (float)width, na.eps);
+    if (!is_finite_f32(total) || !is_finite_f32(inv)) bad = true;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t c = t + j * kRowNormThreads;
+      if (t < kRowNormThreads && c < nchunks) {
+        const uint32_t xw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+        const uint32_t ww[4] = {wv8[j].x, wv8[j].y, wv8[j].z, wv8[j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = norm_weight_bf16(lo_bf16(xw[q]), inv, lo_bf16(ww[q]));
+          const uint32_t hi = norm_weight_bf16(hi_bf16(xw[q]), inv, hi_bf16(ww[q]));
+          bad |= ((lo & 0x7f80u) == 0x7f80u) | ((hi & 0x7f80u) == 0x7f80u);
+          o[q] = lo | (hi << 16);
+        }
+        xs[c] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+    // One workgroup reports what every workgroup sees the same way.
+    if (bad && blockIdx.x == 0 && blockIdx.y == 0) raise_error(err, ERR_NONFINITE);
+    __syncthreads();
+    if (chunks > 0) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        uint32_t sk = u + rot;
+        if (sk >= whole) sk -= whole;
+        xa[u][0] = norm_x(sk);
+      }
+    }
+  } else {
+    if (chunks > 0) load(wa, xa, 0);
+  }
   for (uint32_t c = 0; c < chunks; c += 2) {
     if (c + 1 < chunks) load(wb, xb, (c + 1) * UNROLL);
     __builtin_amdgcn_sched_barrier(0);
@@ -149,8 +291,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(const uint16_t* __rest
     u32x4 wv[NT], xv[MT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) wv[nt] = __builtin_nontemporal_load(wp[nt] + (uint64_t)s * 64);
+    if constexpr (kNorm) {
+      xv[0] = norm_x(s);
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[(uint64_t)s * xkb + mt * 64];
+      for (int mt = 0; mt < MT; ++mt) xv[mt] = xp[(uint64_t)s * xkb + mt * 64];
+    }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -227,10 +373,10 @@ void launch_variant(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t 
   dim3 grid(n / (16 * NT), splits, 1);
   if (m <= 16)
     hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       x_mtiles, residual, out, ldo, err);
+                       x_mtiles, residual, out, ldo, err, RowNormArgs{});
   else
     hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, UNROLL>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb_split,
-                       x_mtiles, residual, out, ldo, err);
+                       x_mtiles, residual, out, ldo, err, RowNormArgs{});
 }
 
 // 32 < m <= 256 (a speculative verify, a small prefill chunk): one split, the
@@ -255,11 +401,11 @@ void launch_wide(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, 
   if (WAVES == 8 && slices * ((m + 63) / 64) > 256) {
     dim3 grid(slices, 1, (m + 31) / 32);
     hipLaunchKernelGGL((gemm_kernel<NT, 2, EPI, WAVES, 4>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb, x_mtiles,
-                       residual, out, ldo, err);
+                       residual, out, ldo, err, RowNormArgs{});
   } else {
     dim3 grid(slices, 1, (m + 63) / 64);
     hipLaunchKernelGGL((gemm_kernel<NT, 4, EPI, WAVES, 2>), grid, dim3(WAVES * 64), 0, s, xt, w, m, kb, kb, x_mtiles,
-                       residual, out, ldo, err);
+                       residual, out, ldo, err, RowNormArgs{});
   }
 }
 
@@ -477,6 +623,48 @@ void launch_panel(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n,
 // activation traffic: 1.41 -> 1.54 ms per step at 32 rows, 1.26 -> 1.42 at
 // one row); the LM head (152K rows) has n-tiles
 // enough for NT = 4 with 4 waves (NT = 2 at up to 16 rows).
+// The weight-streaming variant (n-tiles per wave, waves) launch_epi takes for
+// m <= 32 rows; {0, 0} where it has none.
+struct SmallVariant {
+  uint32_t nt, waves;
+};
+
+SmallVariant small_variant(uint32_t epi, uint32_t m, uint32_t n, uint32_t k, uint32_t splits) {
+  const bool swiglu = epi == FH_EPI_SWIGLU;
+  // Three n-tiles per wave where that puts exactly one workgroup on each of
+  // the 256 CUs and four would leave some idle (the 8B QKV weight: 6144 rows
+  // in 2 splits, 192 -> 256 workgroups, 11.4 -> 10.8 us).
+  if (epi == FH_EPI_PARTIAL && n % 48 == 0 && n / 48 * splits == 256 && (n % 64 != 0 || n / 64 * splits < 256))
+    return {3, 8};
+  if (n < 16384) {
+    const uint32_t waves = (k / 32 + splits - 1) / splits >= 32 ? 8 : 4;
+    auto fills = [&](uint32_t nt) { return n % (16 * nt) == 0 && n / (16 * nt) * splits >= 256; };
+    if (fills(4)) return {4, waves};
+    if (n % 32 == 0 && (fills(2) || swiglu)) return {2, waves};
+    return swiglu ? SmallVariant{0, 0} : SmallVariant{1, waves};
+  }
+  // The LM head: at up to 16 rows (one activation tile) 2 n-tiles per wave
+  // read its 1.24 GB in 182 us instead of 191 (8B, batch 1); at 32 rows 4.
+  if (!swiglu && n % 64 == 0) return {m <= 16 ? 2u : 4u, 4};
+  if (n % 32 == 0) return {2, 4};
+  return swiglu ? SmallVariant{0, 0} : SmallVariant{1, 4};
+}
+
+// Shape policy (measured on MI355X at m = 32, cold weights). Weights of up
+// to 16K rows take the most n-tiles per wave (4, 2, 1) that still give
+// 256 workgroups with the caller's splits (4 keeps the activation traffic
+// at half the weight traffic), or NT = 3 for split-K partials when only
+// that fills the CUs (the 8B QKV weight); the smallest (2 for SwiGLU pairs)
+// when none does. A wave walks at least 4 k-blocks: 8 waves when a split
+// holds 32 k-blocks or more, else 4. The 8B projections keep NT = 4 (3 for
+// QKV) with 8 waves; the Qwen3-0.6B ones, too small to fill the CUs with 4,
+// went (us per launch, 32 rows) from QKV 6.2 to 4.1 (NT 2, 4 waves), O 6.0
+// to 3.3-4.2 (NT 1), gate/up 6.7 to 5.1 (NT 2, 8 waves), down 6.1 to 4.2
+// (NT 1). The fused 8B gate/up weight (24K rows) keeps NT = 2 with 4 waves,
+// twice as many workgroups in flight (NT = 4 with 4 waves, half the
+// activation traffic: 1.41 -> 1.54 ms per step at 32 rows, 1.26 -> 1.42 at
+// one row); the LM head (152K rows) has n-tiles
+// enough for NT = 4 with 4 waves (NT = 2 at up to 16 rows).
 template <int EPI>
 void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, uint32_t k, uint32_t splits,
                 const uint16_t* residual, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
@@ -499,44 +687,88 @@ void launch_epi(const uint16_t* xt, const uint16_t* w, uint32_t m, uint32_t n, u
       return;
     }
   }
-  if constexpr (EPI == FH_EPI_PARTIAL) {
-    // Three n-tiles per wave where that puts exactly one workgroup on each
-    // of the 256 CUs and four would leave some idle (the 8B QKV weight:
-    // 6144 rows in 2 splits, 192 -> 256 workgroups, 11.4 -> 10.8 us).
-    if (n % 48 == 0 && n / 48 * splits == 256 && (n % 64 != 0 || n / 64 * splits < 256)) {
-      launch_variant<3, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
-      return;
+  const SmallVariant v = small_variant(EPI, m, n, k, splits);
+#define FH_VARIANT(NT_, WAVES_) launch_variant<NT_, EPI, WAVES_, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s)
+  if (v.nt == 4) {
+    if (v.waves == 8) FH_VARIANT(4, 8); else FH_VARIANT(4, 4);
+  } else if (v.nt == 2) {
+    if (v.waves == 8) FH_VARIANT(2, 8); else FH_VARIANT(2, 4);
+  } else if constexpr (EPI != FH_EPI_SWIGLU) {
+    if (v.nt == 3) {
+      if constexpr (EPI == FH_EPI_PARTIAL) FH_VARIANT(3, 8);
+    } else if (v.nt == 1) {
+      if (v.waves == 8) FH_VARIANT(1, 8); else FH_VARIANT(1, 4);
     }
   }
-  if (n < 16384) {
-    const bool eight = (k / 32 + splits - 1) / splits >= 32;
-    auto fills = [&](uint32_t nt) { return n % (16 * nt) == 0 && n / (16 * nt) * splits >= 256; };
-#define FH_VARIANT(NT_)                                                                    \
-  do {                                                                                     \
-    if (eight)                                                                             \
-      launch_variant<NT_, EPI, 8, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s); \
-    else                                                                                   \
-      launch_variant<NT_, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s); \
-  } while (0)
-    if (fills(4)) {
-      FH_VARIANT(4);
-    } else if (n % 32 == 0 && (fills(2) || EPI == FH_EPI_SWIGLU)) {
-      FH_VARIANT(2);
-    } else if constexpr (EPI != FH_EPI_SWIGLU) {
-      FH_VARIANT(1);
-    }
 #undef FH_VARIANT
-  } else if (EPI != FH_EPI_SWIGLU && n % 64 == 0) {
-    // The LM head: at up to 16 rows (one activation tile) 2 n-tiles per wave
-    // read its 1.24 GB in 182 us instead of 191 (8B, batch 1); at 32 rows 4.
-    if (m <= 16)
-      launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
-    else
-      launch_variant<4, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
-  } else if (n % 32 == 0) {
-    launch_variant<2, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
-  } else if constexpr (EPI != FH_EPI_SWIGLU) {
-    launch_variant<1, EPI, 4, 4>(xt, w, m, n, k, splits, residual, out, ldo, err, s);
+}
+
+// One row with its residual + RMSNorm in the prologue (launch_gemm_rownorm):
+// the grid and kernel of launch_variant for m = 1, x from the norm.
+template <int NT, int EPI, int WAVES, int NS, int NJ>
+void launch_rownorm_variant(const uint16_t* w, uint32_t n, uint32_t k, uint32_t splits, const RowNormArgs& na,
+                            void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  const uint32_t kb = k / 32;
+  const uint32_t kb_split = (kb + splits - 1) / splits;
+  hipLaunchKernelGGL((gemm_kernel<NT, 1, EPI, WAVES, 4, NS, NJ>), dim3(n / (16 * NT), splits, 1), dim3(WAVES * 64), 0,
+                     s, nullptr, w, 1u, kb, kb_split, 1u, nullptr, out, ldo, err, na);
+}
+
+template <int EPI, int NS, int NJ>
+bool launch_rownorm_ns(SmallVariant v, const uint16_t* w, uint32_t n, uint32_t k, uint32_t splits,
+                       const RowNormArgs& na, void* out, uint32_t ldo, uint32_t* err, hipStream_t s, bool dry) {
+  // The one-row shapes of the Qwen3 projections: QKV (PARTIAL) NT 3 with 8
+  // waves (8B) or NT 2 with 4 (0.6B); gate/up (SWIGLU) NT 2 with 4 or 8
+  // waves; the LM head (F32) NT 2 with 4.
+  if constexpr (EPI == FH_EPI_PARTIAL) {
+    if (v.nt == 3 && v.waves == 8) {
+      if (!dry) launch_rownorm_variant<3, EPI, 8, NS, NJ>(w, n, k, splits, na, out, ldo, err, s);
+      return true;
+    }
+  }
+  if constexpr (EPI == FH_EPI_SWIGLU) {
+    if (v.nt == 2 && v.waves == 8) {
+      if (!dry) launch_rownorm_variant<2, EPI, 8, NS, NJ>(w, n, k, splits, na, out, ldo, err, s);
+      return true;
+    }
+  }
+  if (v.nt == 2 && v.waves == 4) {
+    if (!dry) launch_rownorm_variant<2, EPI, 4, NS, NJ>(w, n, k, splits, na, out, ldo, err, s);
+    return true;
+  }
+  return false;
+}
+
+template <int EPI, int NJ>
+bool launch_rownorm_epi(SmallVariant v, const uint16_t* w, uint32_t n, uint32_t k, uint32_t splits,
+                        const RowNormArgs& na, void* out, uint32_t ldo, uint32_t* err, hipStream_t s, bool dry) {
+  switch (na.splits) {
+    case 0:
+      if constexpr (EPI == FH_EPI_PARTIAL) return launch_rownorm_ns<EPI, 0, NJ>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+      return false;
+    case 4: return launch_rownorm_ns<EPI, 4, NJ>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+    case 6: return launch_rownorm_ns<EPI, 6, NJ>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+    default: return false;
+  }
+}
+
+bool rownorm_dispatch(const uint16_t* w, uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits,
+                      const RowNormArgs& na, void* out, uint32_t ldo, uint32_t* err, hipStream_t s, bool dry) {
+  if (splits == 0 || k % 256 != 0 || k < 1024 || k > 4096 || (epilogue != FH_EPI_PARTIAL && splits != 1))
+    return false;
+  const SmallVariant v = small_variant(epilogue, 1, n, k, splits);
+  const bool two = k / 8 > kRowNormThreads;
+  switch (epilogue) {
+    case FH_EPI_PARTIAL:
+      return two ? launch_rownorm_epi<FH_EPI_PARTIAL, 2>(v, w, n, k, splits, na, out, ldo, err, s, dry)
+                 : launch_rownorm_epi<FH_EPI_PARTIAL, 1>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+    case FH_EPI_SWIGLU:
+      return two ? launch_rownorm_epi<FH_EPI_SWIGLU, 2>(v, w, n, k, splits, na, out, ldo, err, s, dry)
+                 : launch_rownorm_epi<FH_EPI_SWIGLU, 1>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+    case FH_EPI_F32:
+      return two ? launch_rownorm_epi<FH_EPI_F32, 2>(v, w, n, k, splits, na, out, ldo, err, s, dry)
+                 : launch_rownorm_epi<FH_EPI_F32, 1>(v, w, n, k, splits, na, out, ldo, err, s, dry);
+    default: return false;
   }
 }
 
@@ -564,6 +796,19 @@ uint32_t gemm_panel_splits(uint32_t n, uint32_t k) {
   const uint32_t max_s = kb / 16 > 0 ? kb / 16 : 1;
   if (s > max_s) s = max_s;
   return s < 1 ? 1 : s;
+}
+
+bool gemm_rownorm_supported(uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits, uint32_t norm_splits) {
+  RowNormArgs na{};
+  na.splits = norm_splits;
+  return rownorm_dispatch(nullptr, n, k, epilogue, splits, na, nullptr, 0, nullptr, nullptr, true);
+}
+
+hipError_t launch_gemm_rownorm(const uint16_t* w_tiled, uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits,
+                               const RowNormArgs& na, void* out, uint32_t ldo, uint32_t* err, hipStream_t s) {
+  if (na.splits > 0 && na.hidden_out == na.hidden_in) return hipErrorInvalidValue;
+  if (!rownorm_dispatch(w_tiled, n, k, epilogue, splits, na, out, ldo, err, s, false)) return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,

@@ -124,6 +124,31 @@ hipError_t launch_gemm_qkv_rope(const uint16_t* x_tiled, const uint16_t* w_tiled
 hipError_t launch_gemm(const uint16_t* x_tiled, const uint16_t* w_tiled, uint32_t m, uint32_t n, uint32_t k,
                        uint32_t epilogue, uint32_t splits, const uint16_t* residual, void* out, uint32_t ldo,
                        uint32_t* err, hipStream_t s);
+// One row's residual + RMSNorm run by every workgroup of the projection that
+// consumes it (decode steps of one row): hidden_out = bf16((0 + sum of the
+// `splits` slabs of `part`, in split order) + hidden_in) when splits > 0
+// (written by one workgroup; hidden_out must not alias hidden_in), then
+// x = RMSNorm(hidden) with weight w feeds the projection: the arithmetic and
+// order of launch_residual_rmsnorm for that row, bit for bit. splits = 0:
+// x = RMSNorm(hidden_in), nothing written.
+struct RowNormArgs {
+  const uint16_t* hidden_in;
+  uint16_t* hidden_out;
+  const float* part;  // splits slabs of [slab_rows][width] FP32, row 0 used
+  uint32_t splits;
+  uint32_t slab_rows;
+  const uint16_t* w;
+  float eps;
+};
+// The launch launch_gemm picks for m = 1 (same tiles, splits and summation
+// order), with the norm above in the projection's prologue instead of an
+// activation operand. Covered: the epilogues PARTIAL (slab counts 0, 4, 6),
+// SWIGLU and F32 (4, 6) on the tile shapes these take for the Qwen3 widths,
+// k = width in {1024, ..., 4096}, k % 256 == 0; hipErrorInvalidValue
+// otherwise.
+bool gemm_rownorm_supported(uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits, uint32_t norm_splits);
+hipError_t launch_gemm_rownorm(const uint16_t* w_tiled, uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits,
+                               const RowNormArgs& na, void* out, uint32_t ldo, uint32_t* err, hipStream_t s);
 uint32_t gemm_default_splits(uint32_t n, uint32_t k);
 // Split-K factor for kMaxRows < m <= kPanelRows (n % kPanelCols == 0).
 uint32_t gemm_panel_splits(uint32_t n, uint32_t k);

@@ -115,6 +115,23 @@ fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32
                                               error_word, as_stream(stream)));
 }
 
+fh_status fh_op_gemm_rmsnorm(const uint16_t* hidden_in, uint16_t* hidden_out, const float* partials,
+                             uint32_t norm_splits, const uint16_t* norm_weight, float epsilon,
+                             const uint16_t* w_tiled, uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits,
+                             void* out, uint32_t ldo, uint32_t* error_word, void* stream) {
+  if (!hidden_in || !norm_weight || !w_tiled || !out || n == 0 || n % 16) return FH_ERR_INVALID_ARGUMENT;
+  if (norm_splits && (!partials || !hidden_out || hidden_out == hidden_in)) return FH_ERR_INVALID_ARGUMENT;
+  if (epilogue != FH_EPI_SWIGLU && ldo < n) return FH_ERR_INVALID_ARGUMENT;
+  if (!fh::gemm_rownorm_supported(n, k, epilogue, splits, norm_splits)) return FH_ERR_INVALID_ARGUMENT;
+  fh::RowNormArgs na{hidden_in, hidden_out, partials, norm_splits, fh::partial_slab_rows(1), norm_weight, epsilon};
+  return from_hip(fh::launch_gemm_rownorm(w_tiled, n, k, epilogue, splits, na, out, ldo, error_word,
+                                          as_stream(stream)));
+}
+
+uint32_t fh_gemm_rmsnorm_supported(uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits, uint32_t norm_splits) {
+  return n && n % 16 == 0 && fh::gemm_rownorm_supported(n, k, epilogue, splits, norm_splits) ? 1u : 0u;
+}
+
 fh_status fh_op_qknorm_rope_kv(const void* qkv, uint32_t qkv_splits, const uint16_t* q_norm, const uint16_t* k_norm,
                                const float* cos_table, const float* sin_table, const uint32_t* positions,
                                const uint32_t* page_table, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,

@@ -3,7 +3,8 @@
 // replacement for EngineeringTpBatchExecutionV2::forward
 // (adapters/m1-engineering-execution-v1/src/tp_execution/batched.rs:1746-2454).
 //
-// One decode step = 6 + (7, 8 or 9) x layers kernel launches on one HIP
+// One decode step = 6 + (7, 8 or 9) x layers kernel launches (one row:
+// 5 + (5, 6 or 7) x layers, the norms inside the projections) on one HIP
 // stream (enqueue_step; fh_expected_dispatch_count counts the same code
 // without launching), optionally replayed from a HIP graph captured once per
 // row count and attention form. All per-step inputs
@@ -75,6 +76,8 @@ struct fh_ctx {
   float* sin_t = nullptr;
 
   uint16_t* hidden = nullptr;  // residual stream, row-major [cap][hidden]
+  uint16_t* hidden_alt = nullptr;  // one row: the residual stream's other buffer in one-row steps
+  bool row_norm_fused = false;     // one-row steps run each norm in the consuming projection
   uint16_t* xn = nullptr;      // normalized rows, activation tile order
   uint16_t* qrot = nullptr;    // rotated queries, row-major [cap][qh*128]
   uint16_t* attn = nullptr;    // attention output, activation tile order
@@ -476,24 +479,46 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
   const uint32_t meta_words = 2 * cap + R * stride;
   L(FH_KC_EMBEDDING, [&] { return fh::launch_step_ingest(ctx->h_meta, ctx->d_meta, meta_words, err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, ctx->hidden, R, H, md.vocabulary, err, s); });
+  // One row: each residual + RMSNorm runs in the prologue of the projection
+  // that consumes the normalized row (QKV, gate/up, LM head), so a layer is 5
+  // launches. Every workgroup of that projection reads the residual row and
+  // the split-K slabs; one writes the folded row to the residual stream's
+  // other buffer (`cur` alternates between hidden and hidden_alt), so no
+  // workgroup reads a row another one is writing.
+  const bool row_norm = R == 1 && ctx->row_norm_fused;
+  uint16_t* cur = ctx->hidden;
+  auto fold_into = [&](uint32_t slabs) {
+    return slabs == 0 ? cur : cur == ctx->hidden ? ctx->hidden_alt : ctx->hidden;
+  };
+  auto capture_copy = [&](uint32_t layer) {
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_copy_u16(cur, ctx->capture + (uint64_t)layer * ctx->capture_rows * H, (uint64_t)R * H, s);
+    });
+  };
   for (uint32_t l = 0; l < md.layers; ++l) {
     const LayerWeights& W = ctx->layers[l];
     uint16_t* kc = kv_cache(ctx, l, 0);
     uint16_t* vc = kv_cache(ctx, l, 1);
     const uint32_t fold = l == 0 ? 0 : sd;
-    L(FH_KC_RMSNORM, [&] {
-      return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, fold, W.in_norm, ctx->xn, 1, R, H,
-                                         md.rms_epsilon, err, s);
-    });
-    if (ctx->capture && l > 0)
-      L(FH_KC_RMSNORM, [&] {
-        return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(l - 1) * ctx->capture_rows * H,
-                                   (uint64_t)R * H, s);
+    if (row_norm) {
+      uint16_t* next = fold_into(fold);
+      const fh::RowNormArgs na{cur, next, ctx->down_part, fold, fh::partial_slab_rows(1), W.in_norm, md.rms_epsilon};
+      L(FH_KC_QKV_GEMM, [&] {
+        return fh::launch_gemm_rownorm(W.qkv, ctx->nqkv, H, FH_EPI_PARTIAL, sq, na, ctx->qkv_part, ctx->nqkv, err, s);
       });
-    L(FH_KC_QKV_GEMM, [&] {
-      return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part, ctx->nqkv,
-                             err, s);
-    });
+      cur = next;
+      if (ctx->capture && l > 0) capture_copy(l - 1);
+    } else {
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, fold, W.in_norm, ctx->xn, 1, R, H,
+                                           md.rms_epsilon, err, s);
+      });
+      if (ctx->capture && l > 0) capture_copy(l - 1);
+      L(FH_KC_QKV_GEMM, [&] {
+        return fh::launch_gemm(ctx->xn, W.qkv, R, ctx->nqkv, H, FH_EPI_PARTIAL, sq, nullptr, ctx->qkv_part,
+                               ctx->nqkv, err, s);
+      });
+    }
     // Where no row reads another row's new slot, the attention partitions
     // run the QK-norm/RoPE/KV append themselves (same arithmetic, bit for
     // bit), which saves a launch per layer.
@@ -516,30 +541,46 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
     L(FH_KC_O_GEMM, [&] {
       return fh::launch_gemm(ctx->attn, W.o, R, H, Q, FH_EPI_PARTIAL, so, nullptr, ctx->o_part, H, err, s);
     });
-    L(FH_KC_RMSNORM, [&] {
-      return fh::launch_residual_rmsnorm(ctx->hidden, ctx->o_part, so, W.post_norm, ctx->xn, 1, R, H, md.rms_epsilon,
-                                         err, s);
-    });
-    L(FH_KC_GATE_UP_GEMM, [&] {
-      return fh::launch_gemm(ctx->xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, 1, nullptr, ctx->act, I, err, s);
-    });
+    if (row_norm) {
+      uint16_t* next = fold_into(so);
+      const fh::RowNormArgs na{cur, next, ctx->o_part, so, fh::partial_slab_rows(1), W.post_norm, md.rms_epsilon};
+      L(FH_KC_GATE_UP_GEMM, [&] {
+        return fh::launch_gemm_rownorm(W.gu, 2 * I, H, FH_EPI_SWIGLU, 1, na, ctx->act, I, err, s);
+      });
+      cur = next;
+    } else {
+      L(FH_KC_RMSNORM, [&] {
+        return fh::launch_residual_rmsnorm(ctx->hidden, ctx->o_part, so, W.post_norm, ctx->xn, 1, R, H,
+                                           md.rms_epsilon, err, s);
+      });
+      L(FH_KC_GATE_UP_GEMM, [&] {
+        return fh::launch_gemm(ctx->xn, W.gu, R, 2 * I, H, FH_EPI_SWIGLU, 1, nullptr, ctx->act, I, err, s);
+      });
+    }
     L(FH_KC_DOWN_GEMM, [&] {
       return fh::launch_gemm(ctx->act, W.down, R, H, I, FH_EPI_PARTIAL, sd, nullptr, ctx->down_part, H, err, s);
     });
   }
-  L(FH_KC_RMSNORM, [&] {
-    return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, sd, ctx->final_norm, ctx->xn, 1, R, H,
-                                       md.rms_epsilon, err, s);
-  });
-  if (ctx->capture)
-    L(FH_KC_RMSNORM, [&] {
-      return fh::launch_copy_u16(ctx->hidden, ctx->capture + (uint64_t)(md.layers - 1) * ctx->capture_rows * H,
-                                 (uint64_t)R * H, s);
+  if (row_norm) {
+    uint16_t* next = fold_into(sd);
+    const fh::RowNormArgs na{cur, next, ctx->down_part, sd, fh::partial_slab_rows(1), ctx->final_norm, md.rms_epsilon};
+    L(FH_KC_HEAD_GEMM, [&] {
+      return fh::launch_gemm_rownorm(ctx->head, md.vocabulary, H, FH_EPI_F32, 1, na, ctx->logits, md.vocabulary, err,
+                                     s);
     });
-  L(FH_KC_HEAD_GEMM, [&] {
-    return fh::launch_gemm(ctx->xn, ctx->head, R, md.vocabulary, H, FH_EPI_F32, 1, nullptr, ctx->logits,
-                           md.vocabulary, err, s);
-  });
+    cur = next;
+    if (ctx->capture) capture_copy(md.layers - 1);
+  } else {
+    L(FH_KC_RMSNORM, [&] {
+      return fh::launch_residual_rmsnorm(ctx->hidden, ctx->down_part, sd, ctx->final_norm, ctx->xn, 1, R, H,
+                                         md.rms_epsilon, err, s);
+    });
+    if (ctx->capture) capture_copy(md.layers - 1);
+    L(FH_KC_HEAD_GEMM, [&] {
+      return fh::launch_gemm(ctx->xn, ctx->head, R, md.vocabulary, H, FH_EPI_F32, 1, nullptr, ctx->logits,
+                             md.vocabulary, err, s);
+    });
+  }
   L(FH_KC_ARGMAX, [&] {
     return fh::launch_argmax(ctx->logits, R, md.vocabulary, ctx->argmax_scratch, ctx->choices, err, s, ctx->h_out,
                              ctx->h_out + cap);
@@ -659,6 +700,13 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   ctx->s_qkv = fh::gemm_default_splits(ctx->nqkv, H);
   ctx->s_o = fh::gemm_default_splits(H, Q);
   ctx->s_down = fh::gemm_default_splits(H, I);
+  // One-row steps fold and normalize the row inside the QKV, gate/up and LM
+  // head projections where the fused launch covers all of their shapes.
+  ctx->row_norm_fused = fh::gemm_rownorm_supported(ctx->nqkv, H, FH_EPI_PARTIAL, ctx->s_qkv, 0) &&
+                        fh::gemm_rownorm_supported(ctx->nqkv, H, FH_EPI_PARTIAL, ctx->s_qkv, ctx->s_down) &&
+                        fh::gemm_rownorm_supported(2 * I, H, FH_EPI_SWIGLU, 1, ctx->s_o) &&
+                        fh::gemm_rownorm_supported(V, H, FH_EPI_F32, 1, ctx->s_down);
+  if (ctx->row_norm_fused) TRY(dalloc(ctx, &ctx->hidden_alt, H));
   TRY(dalloc(ctx, &ctx->qkv_part, (uint64_t)ctx->s_qkv * kMaxRows * ctx->nqkv));
   TRY(dalloc(ctx, &ctx->o_part, (uint64_t)ctx->s_o * kMaxRows * H));
   TRY(dalloc(ctx, &ctx->down_part, (uint64_t)ctx->s_down * kMaxRows * H));

@@ -273,6 +273,24 @@ fh_status fh_op_residual_rmsnorm(uint16_t* hidden, const float* partials, uint32
                                  uint16_t* y, uint32_t y_tiled, uint32_t rows, uint32_t width, float epsilon,
                                  uint32_t* error_word, void* stream);
 
+/* K2 + K1 for one decode row: the residual + RMSNorm above (rows = 1, width = k) run by
+ * every workgroup of the projection that consumes the normalized row, so the row never
+ * goes through memory between them. When norm_splits > 0, hidden_out = bf16((0 + sum_s
+ * partials[s][0]) + hidden_in) is written (hidden_out must not alias hidden_in); then
+ * out = epilogue(RMSNorm(hidden) . W^T) as fh_op_gemm with m = 1. Bit-identical to
+ * fh_op_residual_rmsnorm followed by fh_op_gemm on the same inputs. Covered: the
+ * projections that follow a norm in a Qwen3 layer (FH_EPI_PARTIAL with the splits
+ * fh_gemm_default_splits gives, norm_splits 0, 4 or 6; FH_EPI_SWIGLU and FH_EPI_F32 with
+ * norm_splits 4 or 6), k = 1024..4096 with k % 256 == 0; FH_ERR_INVALID_ARGUMENT
+ * otherwise. Fuses the two launches the reference makes per norm
+ * (qwen3_rmsnorm_v1 then the projection, batched.rs:1494-1560). */
+fh_status fh_op_gemm_rmsnorm(const uint16_t* hidden_in, uint16_t* hidden_out, const float* partials,
+                             uint32_t norm_splits, const uint16_t* norm_weight, float epsilon,
+                             const uint16_t* w_tiled, uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits,
+                             void* out, uint32_t ldo, uint32_t* error_word, void* stream);
+/* 1 when fh_op_gemm_rmsnorm covers this projection, else 0 (no GPU call). */
+uint32_t fh_gemm_rmsnorm_supported(uint32_t n, uint32_t k, uint32_t epilogue, uint32_t splits, uint32_t norm_splits);
+
 /* K3 per-head QK-norm + split-half RoPE + paged KV append, one launch.
  * qkv: [rows][(qh + 2*kvh) * 128] bf16 projection output when qkv_splits == 0, else
  * qkv_splits FP32 partial slabs of [fh_partial_slab_rows(rows)][(qh + 2*kvh) * 128] (rows <= 256;

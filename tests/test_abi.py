@@ -136,6 +136,23 @@ def test_ops_reject_bad_shapes_before_any_launch():
     assert lib.fh_activation_rows(33) == 256 and lib.fh_activation_rows(257) == 512
     # split-K partial slabs: 32 rows for decode batches, 256 for wide ones, none beyond
     assert [lib.fh_partial_slab_rows(m) for m in (0, 1, 32, 33, 256, 257)] == [0, 32, 32, 256, 256, 0]
+    # one-row projections with the norm in their prologue: the Qwen3 shapes only
+    E = ferric_amd._lib
+    covered = [(6144, 4096, E.EPI_PARTIAL, 2, 0), (6144, 4096, E.EPI_PARTIAL, 2, 4), (24576, 4096, E.EPI_SWIGLU, 1, 4),
+               (151936, 4096, E.EPI_F32, 1, 4), (4096, 1024, E.EPI_PARTIAL, 2, 6), (6144, 1024, E.EPI_SWIGLU, 1, 4),
+               (151936, 1024, E.EPI_F32, 1, 6)]
+    assert all(lib.fh_gemm_rmsnorm_supported(*c) == 1 for c in covered)
+    assert lib.fh_gemm_rmsnorm_supported(6144, 4096, E.EPI_PARTIAL, 2, 3) == 0  # slab count
+    assert lib.fh_gemm_rmsnorm_supported(4096, 4096, E.EPI_PARTIAL, 4, 4) == 0  # the O projection's tiles
+    assert lib.fh_gemm_rmsnorm_supported(6144, 8192, E.EPI_PARTIAL, 2, 4) == 0  # width
+    assert lib.fh_gemm_rmsnorm_supported(6144, 4096, E.EPI_BF16, 1, 4) == 0  # epilogue
+    rn = lambda h_in, h_out, part, ns, n=6144, k=4096, epi=E.EPI_PARTIAL, splits=2: lib.fh_op_gemm_rmsnorm(  # noqa: E731
+        h_in, h_out, part, ns, p, 1e-6, p, n, k, epi, splits, p, n, None, None)
+    q = ctypes.c_void_p(32)
+    assert rn(p, p, q, 4) == 1  # the folded row would overwrite the row being read
+    assert rn(p, q, None, 4) == 1  # slabs missing
+    assert rn(p, None, q, 4) == 1  # no output row
+    assert rn(p, q, q, 3) == 1 and rn(p, q, q, 4, n=4096, splits=4) == 1  # not covered
     ms = ctypes.c_float()
     assert lib.fh_time_attention(None, 1, ctypes.byref(ms)) == 1  # no context
     assert lib.fh_op_rmsnorm(p, p, p, 1, 8200, 1e-6, None, None) == 1

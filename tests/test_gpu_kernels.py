@@ -370,6 +370,78 @@ def test_residual_narrowing_is_the_reference_rounding():
     assert du.to_host(err, np.uint32)[0] != 0  # infinities and NaNs were seen, as the reference rejects
 
 
+# One-row projections with the residual + RMSNorm in their prologue
+# (fh_op_gemm_rmsnorm) on the tile shapes the Qwen3-8B and Qwen3-0.6B one-row
+# steps launch: (n, k, epilogue, splits, norm slabs). The LM head (151936
+# rows) is stood in by 16384 rows, which take the same tiles.
+ROWNORM_CASES = [
+    (6144, 4096, _lib.EPI_PARTIAL, 2, 0), (6144, 4096, _lib.EPI_PARTIAL, 2, 4),  # 8B QKV, layer 0 and after
+    (24576, 4096, _lib.EPI_SWIGLU, 1, 4), (16384, 4096, _lib.EPI_F32, 1, 4),  # 8B gate/up, head
+    (4096, 1024, _lib.EPI_PARTIAL, 2, 0), (4096, 1024, _lib.EPI_PARTIAL, 2, 6),  # 0.6B QKV
+    (6144, 1024, _lib.EPI_SWIGLU, 1, 4), (16384, 1024, _lib.EPI_F32, 1, 6),  # 0.6B gate/up (8 waves), head
+]
+
+
+def _rownorm_pair(n, k, epi, splits, ns, poison=None):
+    """The same row through fh_op_residual_rmsnorm + fh_op_gemm and through
+    fh_op_gemm_rmsnorm: (outputs, folded rows, error words) of each."""
+    r = rng(n + k + ns)
+    hidden = rand_bf16(r, k, 2.0)
+    if poison is not None:
+        hidden[poison] = 0x7FC0
+    w_norm = rand_bf16(r, k, 1.0)
+    slabs = (r.standard_normal((max(ns, 1), 32, k)) * 0.5).astype(np.float32)
+    dt = du.empty(n * k, np.uint16)  # the tiled weight, filled directly (both paths read the same tiles)
+    _lib.check(LIB.fh_op_synth_fill(du.ptr(dt), n * k, orc.synth_tensor_seed(n + k, 3, 1), orc.synth_scale(0.02),
+                                    du.stream()))
+    dp, dwn = du.to_dev(slabs.reshape(-1)), du.to_dev(w_norm)
+    if epi == _lib.EPI_SWIGLU:
+        fill, ldo = np.full(tiled_rows(1) * (n // 2), 0xFFFF, np.uint16), n // 2
+    else:
+        words = splits * 32 * n if epi == _lib.EPI_PARTIAL else n
+        fill, ldo = np.full(words, np.nan, np.float32), n
+    # two launches
+    dh, dy = du.to_dev(hidden), du.empty(tiled_rows(1) * k, np.uint16)
+    out_a, err_a = du.to_dev(fill), du.to_dev(np.zeros(1, np.uint32))
+    _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp) if ns else None, ns, du.ptr(dwn), du.ptr(dy), 1, 1,
+                                          k, 1e-6, du.ptr(err_a), du.stream()))
+    _lib.check(LIB.fh_op_gemm(du.ptr(dy), du.ptr(dt), 1, n, k, epi, splits, None, du.ptr(out_a), ldo, du.ptr(err_a),
+                              du.stream()))
+    # one launch
+    dh_in, dh_out = du.to_dev(hidden), du.to_dev(np.full(k, 0xFFFF, np.uint16))
+    out_b, err_b = du.to_dev(fill), du.to_dev(np.zeros(1, np.uint32))
+    _lib.check(LIB.fh_op_gemm_rmsnorm(du.ptr(dh_in), du.ptr(dh_out), du.ptr(dp) if ns else None, ns, du.ptr(dwn),
+                                      1e-6, du.ptr(dt), n, k, epi, splits, du.ptr(out_b), ldo, du.ptr(err_b),
+                                      du.stream()))
+    dtype = np.uint16 if epi == _lib.EPI_SWIGLU else np.uint32
+    assert np.array_equal(du.to_host(dh_in, np.uint16), hidden)  # the input row is never written
+    return ((du.to_host(out_a, dtype), du.to_host(dh, np.uint16), int(du.to_host(err_a, np.uint32)[0])),
+            (du.to_host(out_b, dtype), du.to_host(dh_out, np.uint16), int(du.to_host(err_b, np.uint32)[0])))
+
+
+@pytest.mark.parametrize("n,k,epi,splits,ns", ROWNORM_CASES)
+def test_gemm_rmsnorm_equals_the_two_launches(n, k, epi, splits, ns):
+    # Bar: bit-equal outputs (every slab, bf16 tile or FP32 logit, untouched
+    # words included), folded residual row and error word: the fused launch
+    # keeps both kernels' arithmetic and summation order.
+    assert LIB.fh_gemm_rmsnorm_supported(n, k, epi, splits, ns) == 1
+    (out_a, h_a, err_a), (out_b, h_b, err_b) = _rownorm_pair(n, k, epi, splits, ns)
+    assert err_a == 0 and err_b == 0
+    diff = np.flatnonzero(out_a != out_b)
+    assert diff.size == 0, (diff.size, diff[:8])
+    if ns:
+        assert np.array_equal(h_b, h_a)
+    else:
+        assert np.all(h_b == 0xFFFF)  # no slabs: nothing folded, nothing written
+
+
+@pytest.mark.parametrize("n,k,epi,splits,ns", [ROWNORM_CASES[1], ROWNORM_CASES[6]])
+def test_gemm_rmsnorm_reports_nonfinite_rows(n, k, epi, splits, ns):
+    # A NaN in the residual row: both paths raise the nonfinite bit.
+    (_, _, err_a), (_, _, err_b) = _rownorm_pair(n, k, epi, splits, ns, poison=5)
+    assert err_a != 0 and err_b == err_a
+
+
 def _paged_pool(r, pages, kvh, scale=1.0):
     n = pages * 16 * kvh * 128
     return rand_bf16(r, n, scale), rand_bf16(r, n, scale)

@@ -410,6 +410,36 @@ def test_qwen3_0_6b_batch32_decode_steps():
         pair.close()
 
 
+def test_one_row_steps_with_norms_in_the_projections():
+    # One-row steps run every residual + RMSNorm inside the projection after
+    # it, the residual stream alternating between two buffers: 4 steps of one
+    # row (positions 0 and 700 on), eager and replayed from the graph, must
+    # give bit-identical captured layers and logits, each step within the
+    # oracle bars, and the written KV slots checked afterwards.
+    cfg = dict(ferric_amd.QWEN3_0_6B, layers=3)
+    limits = PagedLimits(context_tokens=1024, physical_page_count=128, page_table_stride=64)
+    runs = []
+    for graphs in (False, True):
+        pair = Pair(cfg, limits, seed=13, graphs=graphs, rows=4)
+        try:
+            sids = pair.admit_with_prefix([0, 700])
+            tok, logits, hidden = [17, 4242], [], []
+            for step in range(4):
+                row = step % 2
+                batch, out, ref = pair.step([(sids[row], tok[row])])
+                _mark_written(pair, batch)
+                pair.check(batch, out, ref, f"one row, graphs {graphs}, step {step}")
+                tok[row] = int(ref["choices"][0])
+                logits.append(pair.gpu.read_logits().copy())
+                hidden.append(np.stack([pair.gpu.read_hidden(l) for l in range(cfg["layers"])]))
+            pair.check_kv()
+            runs.append((np.stack(logits), np.stack(hidden)))
+        finally:
+            pair.close()
+    assert np.array_equal(runs[0][0].view(np.uint32), runs[1][0].view(np.uint32))
+    assert np.array_equal(runs[0][1], runs[1][1])
+
+
 def test_graph_replay_is_bit_identical_to_eager():
     cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
     limits = PagedLimits(context_tokens=512, physical_page_count=64, page_table_stride=32)
