@@ -76,7 +76,8 @@ __global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(const float
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pval,
                                                           const uint32_t* __restrict__ pidx,
                                                           uint32_t* __restrict__ choices, uint32_t* err,
-                                                          uint32_t* host_choices, uint32_t* host_err) {
+                                                          uint32_t* host_choices, uint32_t* host_err,
+                                                          uint32_t* host_done) {
   const uint32_t row = blockIdx.x;
   Cand c{pval[row * kArgmaxShards + threadIdx.x], pidx[row * kArgmaxShards + threadIdx.x]};
   c = wave_best(c);
@@ -93,6 +94,9 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
         const uint32_t e = err ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         __hip_atomic_store(host_err, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
+      // Published after this row's stores above: a host that sees the word
+      // set reads this row's choice (and, for row 0, the error word).
+      if (host_done) __hip_atomic_store(host_done + row, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
@@ -100,7 +104,8 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 }  // namespace
 
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
-                         uint32_t* err, hipStream_t s, uint32_t* host_choices, uint32_t* host_err) {
+                         uint32_t* err, hipStream_t s, uint32_t* host_choices, uint32_t* host_err,
+                         uint32_t* host_done) {
   float* pval = reinterpret_cast<float*>(scratch);
   uint32_t* pidx = reinterpret_cast<uint32_t*>(pval + (uint64_t)rows * kArgmaxShards);
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxShards, rows), dim3(kArgThreads), 0, s, logits, vocab, pval,
@@ -108,7 +113,7 @@ hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, voi
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, pval, pidx, choices, err,
-                     host_choices, host_err);
+                     host_choices, host_err, host_done);
   return hipGetLastError();
 }
 

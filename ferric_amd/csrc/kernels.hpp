@@ -210,9 +210,12 @@ hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, c
 
 // logits
 // With host_choices (coherent pinned memory), the choices and the error word
-// (at host_err) are also stored there, so the host reads them after the
-// stream synchronizes without a device-to-host copy.
+// (at host_err) are also stored there, so the host reads them without a
+// device-to-host copy; with host_done, row r's word is then set to 1 with a
+// system-scope release (row 0's after the error word too), so a host that
+// sees every row's word set reads complete choices and error bits.
 hipError_t launch_argmax(const float* logits, uint32_t rows, uint32_t vocab, void* scratch, uint32_t* choices,
-                         uint32_t* err, hipStream_t s, uint32_t* host_choices = nullptr, uint32_t* host_err = nullptr);
+                         uint32_t* err, hipStream_t s, uint32_t* host_choices = nullptr, uint32_t* host_err = nullptr,
+                         uint32_t* host_done = nullptr);
 
 }  // namespace fh

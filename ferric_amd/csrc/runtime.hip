@@ -14,6 +14,7 @@
 // graph stays valid across steps and a step needs no copy beside it.
 // Prefill chunks (run_prefill) keep a host-to-device copy of their metadata.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -97,7 +98,7 @@ struct fh_ctx {
 
   uint32_t* d_meta = nullptr;  // tokens[cap] | positions[cap] | table[cap][stride]
   uint32_t* h_meta = nullptr;  // pinned mirror
-  uint32_t* h_out = nullptr;   // pinned: choices[cap] | error word
+  uint32_t* h_out = nullptr;   // pinned: choices[cap] | error word | done[cap] (one word per row)
 
   // Prefill chunks (row_capacity < rows <= prefill_rows); allocated only when
   // prefill_rows > 0. Activation-tile buffers hold act_mtiles(prefill_rows) tiles.
@@ -583,7 +584,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
   }
   L(FH_KC_ARGMAX, [&] {
     return fh::launch_argmax(ctx->logits, R, md.vocabulary, ctx->argmax_scratch, ctx->choices, err, s, ctx->h_out,
-                             ctx->h_out + cap);
+                             ctx->h_out + cap, ctx->h_out + cap + 1);
   });
   ++n;  // argmax is two launches
   *launches = n;
@@ -725,7 +726,7 @@ fh_status fh_create(const fh_model_desc* md_in, const fh_ctx_options* op_in, fh_
   // Decode steps read their metadata from, and publish their choices into,
   // these two buffers from inside the step's kernels: coherent pinned memory.
   TRY(halloc(ctx, &ctx->h_meta, meta, hipHostMallocCoherent));
-  TRY(halloc(ctx, &ctx->h_out, cap + 1, hipHostMallocCoherent));
+  TRY(halloc(ctx, &ctx->h_out, 2 * cap + 1, hipHostMallocCoherent));
   if (op.prefill_rows) {
     auto& p = ctx->pre;
     const uint32_t P = op.prefill_rows;
@@ -1179,6 +1180,23 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   return FH_OK;
 }
 
+// Polls the per-row words the step's last launch sets once its choices are
+// stored (coherent pinned memory), so the calling thread is running when the
+// step ends instead of being woken from a blocking wait: measured on MI355X,
+// waking from hipStreamSynchronize added 50-180 us to a 3.3 ms step. The
+// thread spins for at most kChoicesSpinMs; the stream synchronize that
+// follows then waits, and reports errors, as before.
+constexpr int kChoicesSpinMs = 100;
+
+void await_choices(const uint32_t* done, uint32_t rows) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint32_t i = 0; i < rows; ++i)
+    while (__atomic_load_n(done + i, __ATOMIC_ACQUIRE) == 0u) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(kChoicesSpinMs)) return;
+      __builtin_ia32_pause();
+    }
+}
+
 fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32_t nrows,
                            const uint32_t* output_rows, uint32_t nout, uint32_t* choices_out) {
   if (!ctx) return FH_ERR_INVALID_ARGUMENT;
@@ -1204,6 +1222,8 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   };
   hipStream_t s = ctx->stream;
   hipError_t e = hipSuccess;
+  uint32_t* done = ctx->h_out + cap + 1;
+  for (uint32_t i = 0; i < nrows; ++i) __atomic_store_n(done + i, 0u, __ATOMIC_RELAXED);
   hipEventRecord(ctx->ev_begin, s);
   uint64_t launches = 0;
   if (ctx->profiling) ctx->prof_launches.clear();
@@ -1236,6 +1256,7 @@ fh_status fh_execute_batch(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, u
   if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + ctx->launch_detail);
   hipEventRecord(ctx->ev_end, s);
   // The step's first launch read h_meta and its last one wrote h_out.
+  await_choices(done, nrows);
   e = hipStreamSynchronize(s);
   if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("step: ") + hipGetErrorString(e));
   hipEventElapsedTime(&ctx->last_ms, ctx->ev_begin, ctx->ev_end);

@@ -75,21 +75,88 @@ class PagePool:
         (a row whose position starts a page the sequence does not have yet
         takes the next free page). Every row of a sequence sees the
         sequence's full reserved page list, as a read-only snapshot."""
+        if len(rows) <= 4:
+            return self._prepare_small(rows)
         if len(rows) <= 256:
-            cols = self._prepare_loop(rows)
+            cols = self._prepare_distinct(rows) or self._prepare_loop(rows)
         else:
             cols = self._prepare_vector(rows)
         states, sid, token, pos, group = cols
+        if len(token) and (int(token.min()) < 0 or int(token.max()) > 0xFFFFFFFF):
+            raise ValueError("token outside u32")
         lens = np.fromiter([st._count for st in states], dtype=np.int64, count=len(states))
         offs = np.zeros(len(states), dtype=np.int64)
         if len(states) > 1:
             np.cumsum(lens[:-1], out=offs[1:])
         tables = np.concatenate([st._view for st in states]) if states else np.zeros(0, np.uint32)
         writable = tables[offs[group] + pos // PAGE_TOKENS] if len(token) else np.zeros(0, np.uint32)
-        prepared = PreparedRows(sid, token, pos, writable, tables, offs, lens, group)
+        prepared = PreparedRows._trusted(sid.astype(np.uint64), token.astype(np.uint32), pos.astype(np.uint32),
+                                         writable, tables, offs, lens, group)
         bid = self._next_batch
         self._next_batch += 1
         return PreparedBatch(bid, prepared, self.limits)
+
+    def _prepare_small(self, rows: list) -> PreparedBatch:
+        """prepare() for a few rows (a batch-1 decode step): the row loop's
+        bookkeeping on Python lists, one small array per column, and a
+        lone sequence's page list handed over as a view of its table (the
+        entries a view covers never change: pages are only appended)."""
+        sequences = self.sequences
+        group_of: dict[int, int] = {}
+        states, next_pos = [], []
+        sid, token, pos, group = [], [], [], []
+        for s, t in rows:
+            t = int(t)
+            if not 0 <= t <= 0xFFFFFFFF:
+                raise ValueError("token outside u32")
+            g = group_of.get(s)
+            if g is None:
+                g = group_of[s] = len(states)
+                st = sequences[s]
+                states.append(st)
+                next_pos.append(st.length)
+            else:
+                st = states[g]
+            p = next_pos[g]
+            next_pos[g] = p + 1
+            if p // PAGE_TOKENS >= st._count:
+                self._ensure(st, p + 1)
+            sid.append(s)
+            token.append(t)
+            pos.append(p)
+            group.append(g)
+        lens = [st._count for st in states]
+        offs = [0] * len(states)
+        for g in range(1, len(states)):
+            offs[g] = offs[g - 1] + lens[g - 1]
+        if len(states) == 1:
+            tables = states[0]._table[: lens[0]]
+        else:
+            tables = np.concatenate([st._view for st in states]) if states else np.zeros(0, np.uint32)
+        writable = [int(tables[offs[g] + p // PAGE_TOKENS]) for g, p in zip(group, pos)]
+        prepared = PreparedRows._trusted(np.array(sid, np.uint64), np.array(token, np.uint32), np.array(pos, np.uint32),
+                                         np.array(writable, np.uint32), tables, np.array(offs, np.int64),
+                                         np.array(lens, np.int64), np.array(group, np.int64))
+        bid = self._next_batch
+        self._next_batch += 1
+        return PreparedBatch(bid, prepared, self.limits)
+
+    def _prepare_distinct(self, rows: list):
+        """The row loop's columns for a batch whose rows all belong to
+        different sequences (a decode step), with one comprehension per
+        column; None when a sequence repeats."""
+        sequences = self.sequences
+        sid = [r[0] for r in rows]
+        states = [sequences[s] for s in sid]
+        if len(set(sid)) != len(sid):
+            return None
+        pos = [st.length for st in states]
+        for st, p in zip(states, pos):
+            if p // PAGE_TOKENS >= st._count:
+                self._ensure(st, p + 1)
+        n = len(rows)
+        return (states, np.array(sid, dtype=np.int64), np.array([int(r[1]) for r in rows], dtype=np.int64),
+                np.array(pos, dtype=np.int64), np.arange(n, dtype=np.int64))
 
     def _prepare_loop(self, rows: list):
         sequences = self.sequences

@@ -79,6 +79,18 @@ class PreparedRows(_SequenceABC):
         self.table_len = np.asarray(table_len, dtype=np.int64)
         self.table_index = np.asarray(table_index, dtype=np.int64)
 
+    @classmethod
+    def _trusted(cls, sequence, token, position, writable, tables, table_offset, table_len, table_index):
+        """The same object from columns that already have the final dtypes
+        (uint64 sequence, uint32 token/position/writable/tables, int64
+        offsets, lengths and indices) and token ids the caller checked: the
+        page pool's path, which runs once per decode step."""
+        self = cls.__new__(cls)
+        self.sequence, self.token, self.position, self.writable = sequence, token, position, writable
+        tables.flags.writeable = False
+        self.tables, self.table_offset, self.table_len, self.table_index = tables, table_offset, table_len, table_index
+        return self
+
     def __len__(self) -> int:
         return len(self.token)
 
@@ -128,9 +140,30 @@ ROW_DTYPE = np.dtype([("sequence", "<u8"), ("token", "<u4"), ("position", "<u4")
                       ("page_count", "<u4"), ("writable_page", "<u4")])
 
 
+class _RowWords(ctypes.Structure):
+    """fh_row with the page list as a plain address (same layout as _lib.Row)."""
+
+    _fields_ = [("sequence", ctypes.c_uint64), ("token", ctypes.c_uint32), ("position", ctypes.c_uint32),
+                ("pages", ctypes.c_uint64), ("page_count", ctypes.c_uint32), ("writable_page", ctypes.c_uint32)]
+
+
+_SMALL_BATCH = 4  # rows up to which a batch is marshalled field by field (cheaper than column copies)
+
+
 def _rows_to_c(rows: Sequence[PreparedRow]):
     """fh_row[] for the C ABI; returns (pointer, objects that must stay alive)."""
     n = len(rows)
+    if isinstance(rows, PreparedRows) and 0 < n <= _SMALL_BATCH:
+        arr = (_RowWords * n)()
+        base = rows.tables.__array_interface__["data"][0]
+        seq, tok, pos, wr = rows.sequence.tolist(), rows.token.tolist(), rows.position.tolist(), rows.writable.tolist()
+        grp, offs, lens = rows.table_index.tolist(), rows.table_offset.tolist(), rows.table_len.tolist()
+        for i in range(n):
+            r, g = arr[i], grp[i]
+            r.sequence, r.token, r.position, r.writable_page = seq[i], tok[i], pos[i], wr[i]
+            r.page_count = lens[g]
+            r.pages = base + 4 * offs[g] if lens[g] else 0
+        return ctypes.cast(arr, ctypes.POINTER(_lib.Row)), [arr, rows.tables]
     rec = np.zeros(max(n, 1), dtype=ROW_DTYPE)
     keep = [rec]
     if isinstance(rows, PreparedRows):

@@ -310,6 +310,40 @@ int orc_rmsnorm_wave(const uint16_t* input, const uint16_t* weight, uint32_t row
   return 0;
 }
 
+// Pure RMSNorm whose sum of squares is taken exactly: the squares rounded to
+// FP32 as the reference forms them (rmsnorm.rs:421-438), summed in double
+// (exact to well below an FP32 ulp for rows of up to 8192 squares), rounded
+// to FP32 once; the inverse and the normalize-and-weight steps are the serial
+// ones. The most accurate reassociation of the reference's sum, so one more
+// point of its arithmetic's legal spread. Returns 1 where the reference traps.
+int orc_rmsnorm_exact(const uint16_t* input, const uint16_t* weight, uint32_t rows, uint32_t width, float eps,
+                      uint16_t* norm_out) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint64_t base = (uint64_t)r * width;
+    double acc = 0.0;
+    for (uint32_t c = 0; c < width; ++c) {
+      const float x = widen(input[base + c]);
+      const float sq = x * x;
+      if (!finite(x) || !finite(sq)) return 1;
+      acc += (double)sq;
+    }
+    const float sum = (float)acc;
+    const float mean_square = sum / (float)width;
+    const float stabilized = mean_square + eps;
+    const float denominator = std::sqrt(stabilized);
+    const float inverse = 1.0f / denominator;
+    if (!finite(sum) || !finite(mean_square) || !finite(stabilized) || stabilized <= 0.f || !finite(denominator) ||
+        denominator <= 0.f || !finite(inverse))
+      return 1;
+    for (uint32_t c = 0; c < width; ++c) {
+      const uint32_t o = orc_norm_weight(widen(input[base + c]) * inverse, weight[c]);
+      if (o == 0xffffffffu) return 1;
+      norm_out[base + c] = (uint16_t)o;
+    }
+  }
+  return 0;
+}
+
 // ferric_qwen3_token_embedding_bf16_copy_v1 (gemm.rs:768-853): bit copy;
 // returns the first row whose token is out of range + 1, or 0.
 uint32_t orc_embedding(const uint32_t* tokens, const uint16_t* weight, uint32_t rows, uint32_t hidden,
@@ -847,6 +881,7 @@ static void model_gemm(OrcModel* m, const uint16_t* a, const uint16_t* b, uint32
 
 static int model_norm(OrcModel* m, const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_t width,
                       uint16_t* out) {
+  if (m->order == 3) return orc_rmsnorm_exact(x, w, rows, width, m->eps, out);
   if (m->order >= 1) return orc_rmsnorm_wave(x, w, rows, width, m->eps, out);
   return orc_rmsnorm(x, nullptr, w, rows, width, m->eps, 0, nullptr, out);
 }

@@ -94,6 +94,8 @@ def lib():
         L.orc_square_sum_wave.restype = ctypes.c_float
         L.orc_rmsnorm_wave.argtypes = [_u16p, _u16p, _c_u32, _c_u32, ctypes.c_float, _u16p]
         L.orc_rmsnorm_wave.restype = ctypes.c_int
+        L.orc_rmsnorm_exact.argtypes = [_u16p, _u16p, _c_u32, _c_u32, ctypes.c_float, _u16p]
+        L.orc_rmsnorm_exact.restype = ctypes.c_int
         L.orc_attention_head_wave.argtypes = [_u16p, _u16p, _u16p, _u32p, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32,
                                               _u16p]
         L.orc_attention_head_wave.restype = ctypes.c_int
@@ -159,6 +161,15 @@ def rmsnorm_wave(x, weight, rows, width, eps=1e-6):
     weight = np.ascontiguousarray(weight, dtype=np.uint16)
     out = np.zeros(rows * width, dtype=np.uint16)
     st = lib().orc_rmsnorm_wave(_ptr(x, _u16p), _ptr(weight, _u16p), rows, width, eps, _ptr(out, _u16p))
+    return None if st else out
+
+
+def rmsnorm_exact(x, weight, rows, width, eps=1e-6):
+    """RMSNorm with the sum of squares taken exactly (float64, one rounding)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    weight = np.ascontiguousarray(weight, dtype=np.uint16)
+    out = np.zeros(rows * width, dtype=np.uint16)
+    st = lib().orc_rmsnorm_exact(_ptr(x, _u16p), _ptr(weight, _u16p), rows, width, eps, _ptr(out, _u16p))
     return None if st else out
 
 
@@ -381,7 +392,9 @@ class Model:
         """Reduction order of later calls: 0 = the reference's serial (v1)
         sums, 1 = its wave-order profiles (v5 GEMV, v15 RMSNorm, v14 attention),
         2 = order 1 with a planted mistake (gate/up narrowed by truncation), for
-        tests that show a drift bound catches a 1-ulp-biased rounding."""
+        tests that show a drift bound catches a 1-ulp-biased rounding, 3 =
+        order 1 with every RMSNorm's sum of squares taken exactly (the most
+        accurate reassociation of the reference's sum)."""
         lib().orc_model_set_order(self.h, int(order))
 
     def layer_isolated(self, layer, hidden_in, positions, tables, page_counts, stride, order=None, kv=None):

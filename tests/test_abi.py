@@ -217,6 +217,19 @@ def test_page_pool_large_batch_matches_row_loop():
         rows = [(sids[i], int(t)) for i, t in zip(rng.integers(0, 5, 600), rng.integers(0, 151936, 600))]
         return pool, rows
 
+    # A decode step (every row a different sequence) takes the per-column path.
+    for pick in ([0, 1, 2, 3, 4], [4, 2, 0, 3, 1]):
+        pool_a, _ = build()
+        pool_b, _ = build()
+        sa, sb = sorted(pool_a.sequences), sorted(pool_b.sequences)
+        ca = pool_a._prepare_distinct([(sa[i], 100 + i) for i in pick])
+        cb = pool_b._prepare_loop([(sb[i], 100 + i) for i in pick])
+        assert [st.sequence for st in ca[0]] == [st.sequence for st in cb[0]]
+        for x, y in zip(ca[1:], cb[1:]):
+            np.testing.assert_array_equal(x, y)
+        assert pool_a.free == pool_b.free
+    pool_a, _ = build()
+    assert pool_a._prepare_distinct([(1, 5), (2, 6), (1, 7)]) is None  # a repeated sequence
     pool_a, rows = build()
     pool_b, _ = build()
     cols_a = pool_a._prepare_vector(rows)
@@ -234,6 +247,52 @@ def test_page_pool_large_batch_matches_row_loop():
     assert not r.physical_pages.flags.writeable
     with pytest.raises(ValueError):
         pool_a.prepare([(rows[0][0], -1)] * 300)
+
+
+def test_page_pool_small_batches_match_the_general_path():
+    # Up to 4 rows are prepared and marshalled on a short path (a batch-1
+    # decode step runs it every step); it must give the columns, page lists,
+    # allocations and fh_row records of the general path.
+    import ctypes
+
+    from ferric_amd.runner import _rows_to_c
+
+    limits = PagedLimits(context_tokens=1024, physical_page_count=200, page_table_stride=64)
+
+    def build():
+        pool = PagePool(limits, seed=5)
+        return pool, [pool.admit(n) for n in (0, 15, 16, 47, 300)]
+
+    for rows_of in ([(0, 7)], [(1, 9)], [(4, 3), (4, 4)], [(2, 1), (1, 2), (2, 3), (0, 4)], [(3, 8), (3, 9)]):
+        pool_a, sa = build()
+        pool_b, sb = build()
+        rows_a = [(sa[i], t) for i, t in rows_of]
+        rows_b = [(sb[i], t) for i, t in rows_of]
+        small = pool_a.prepare(rows_a).rows
+        states, sid, token, pos, group = pool_b._prepare_loop(rows_b)
+        assert pool_a.free == pool_b.free
+        for s_a, s_b in zip(sa, sb):
+            np.testing.assert_array_equal(pool_a.sequences[s_a].pages, pool_b.sequences[s_b].pages)
+        np.testing.assert_array_equal(small.token, token)
+        np.testing.assert_array_equal(small.position, pos)
+        np.testing.assert_array_equal(small.table_index, group)
+        assert small.token.dtype == np.uint32 and small.sequence.dtype == np.uint64
+        for i, r in enumerate(small):
+            np.testing.assert_array_equal(r.physical_pages, states[group[i]].pages)
+            assert r.writable_physical_page == r.physical_pages[r.position // 16]
+            assert not r.physical_pages.flags.writeable
+        ptr, keep = _rows_to_c(small)
+        for i, r in enumerate(small):
+            c = ptr[i]
+            assert (c.sequence, c.token, c.position, c.page_count, c.writable_page) == (
+                r.sequence, r.token, r.position, len(r.physical_pages), r.writable_physical_page)
+            assert list(c.pages[: c.page_count]) == list(r.physical_pages)
+            assert ctypes.addressof(c.pages.contents) == r.physical_pages.__array_interface__["data"][0]
+    pool, s = build()
+    with pytest.raises(ValueError):
+        pool.prepare([(s[0], -1)])
+    with pytest.raises(ValueError):
+        pool.prepare([(s[0], 1 << 32)])
 
 
 def test_library_shares_torch_hip_runtime():

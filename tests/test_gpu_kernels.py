@@ -442,6 +442,77 @@ def test_gemm_rmsnorm_reports_nonfinite_rows(n, k, epi, splits, ns):
     assert err_a != 0 and err_b == err_a
 
 
+@pytest.mark.parametrize("n,k,epi,ns", [(151936, 4096, _lib.EPI_F32, 4), (151936, 1024, _lib.EPI_F32, 6),
+                                        (24576, 4096, _lib.EPI_SWIGLU, 4), (6144, 4096, _lib.EPI_PARTIAL, 4)])
+def test_one_row_projections_at_full_width_match_oracle(n, k, epi, ns):
+    # The one-row projections at the full Qwen3 widths (the LM head's 151936
+    # rows at both model widths, the 8B gate/up and QKV) against the oracle:
+    # the fused norm + projection and the two launches. Weights are
+    # synthesized on the device untiled and tiled there; the oracle
+    # regenerates them. Bars: FP32 outputs within F32_BOUND, SwiGLU within 3
+    # bf16 ulps (as the GEMM tests above), the folded row bit-exact.
+    r = rng(n + ns)
+    splits = int(LIB.fh_gemm_default_splits(n, k)) if epi == _lib.EPI_PARTIAL else 1
+    ts, scale = orc.synth_tensor_seed(n + k, 9, 1), orc.synth_scale(0.02)
+    dw, dt = du.empty(n * k, np.uint16), du.empty(n * k, np.uint16)
+    _lib.check(LIB.fh_op_synth_fill(du.ptr(dw), n * k, ts, scale, du.stream()))
+    if epi == _lib.EPI_SWIGLU:
+        _lib.check(LIB.fh_op_tile_gate_up(du.ptr(dw), du.ptr(dw) + (n // 2) * k * 2, du.ptr(dt), n // 2, k, du.stream()))
+    else:
+        _lib.check(LIB.fh_op_tile_weight(du.ptr(dw), du.ptr(dt), n, k, du.stream()))
+    del dw
+    w = orc.synth(n * k, ts, scale)
+    hidden, w_norm = rand_bf16(r, k, 2.0), rand_bf16(r, k, 1.0)
+    slabs = (r.standard_normal((ns, 32, k)) * 0.5).astype(np.float32)
+    total = slabs[0, 0].copy()
+    for sp in range(1, ns):
+        total = (total + slabs[sp, 0]).astype(np.float32)
+    h_exp = orc.residual(total, hidden)
+    x = orc.rmsnorm(h_exp, w_norm, 1, k)
+    if epi == _lib.EPI_SWIGLU:
+        i = n // 2
+        ref = orc.swiglu(orc.gemm(x, w[: i * k], 1, i, k), orc.gemm(x, w[i * k:], 1, i, k))
+        fill, ldo = np.full(tiled_rows(1) * i, 0xFFFF, np.uint16), i
+    else:
+        ref = orc.gemm(x, w, 1, n, k, f32_out=True)
+        fill, ldo = np.full(splits * 32 * n if epi == _lib.EPI_PARTIAL else n, np.nan, np.float32), n
+    del w
+    dp, dwn = du.to_dev(slabs.reshape(-1)), du.to_dev(w_norm)
+
+    def outputs(out):
+        if epi == _lib.EPI_SWIGLU:
+            o = du.empty(n // 2, np.uint16)
+            _lib.check(LIB.fh_op_untile_activation(du.ptr(out), du.ptr(o), 1, n // 2, du.stream()))
+            return du.to_host(o, np.uint16)
+        got = du.to_host(out, np.float32)
+        if epi == _lib.EPI_PARTIAL:
+            s = got.reshape(splits, 32, n)[:, 0]
+            acc = s[0].copy()
+            for sp in range(1, splits):
+                acc = (acc + s[sp]).astype(np.float32)
+            return acc
+        return got
+
+    def check(got, label):
+        if epi == _lib.EPI_SWIGLU:
+            assert du.bf16_close(got, ref, ulps=3), label
+        else:
+            err = np.abs(got.astype(np.float64) - ref)
+            assert np.max(err) <= F32_BOUND, (label, float(np.max(err)), int(np.argmax(err)))
+
+    dh_in, dh_out, out, err = du.to_dev(hidden), du.empty(k, np.uint16), du.to_dev(fill), du.empty(1, np.uint32)
+    _lib.check(LIB.fh_op_gemm_rmsnorm(du.ptr(dh_in), du.ptr(dh_out), du.ptr(dp), ns, du.ptr(dwn), 1e-6, du.ptr(dt), n,
+                                      k, epi, splits, du.ptr(out), ldo, du.ptr(err), du.stream()))
+    assert du.to_host(err, np.uint32)[0] == 0
+    assert np.array_equal(du.to_host(dh_out, np.uint16), h_exp)
+    check(outputs(out), "fused")
+    dh, dy, out2 = du.to_dev(hidden), du.empty(tiled_rows(1) * k, np.uint16), du.to_dev(fill)
+    _lib.check(LIB.fh_op_residual_rmsnorm(du.ptr(dh), du.ptr(dp), ns, du.ptr(dwn), du.ptr(dy), 1, 1, k, 1e-6, None,
+                                          du.stream()))
+    _lib.check(LIB.fh_op_gemm(du.ptr(dy), du.ptr(dt), 1, n, k, epi, splits, None, du.ptr(out2), ldo, None, du.stream()))
+    check(outputs(out2), "two launches")
+
+
 def _paged_pool(r, pages, kvh, scale=1.0):
     n = pages * 16 * kvh * 128
     return rand_bf16(r, n, scale), rand_bf16(r, n, scale)

@@ -186,14 +186,22 @@ class Pair:
               f"wave {np.mean(self.rms_wave):.3e}")
         sp.check_layer_errors(self.rms_gpu, self.rms_wave, label)
         # The head's own error, on the GPU's final residual stream of the output rows.
+        # The spread is the larger of two legal orders' differences from the
+        # serial head: the wave order's, and the exactly summed final norm's
+        # (order 3). One row's final norm can flip a few dozen elements by an
+        # ulp between orders (repeated mantissas sit on the same rounding
+        # boundary) while the serial and wave sums happen to agree.
         final = hidden[-1][outs]
         iso = self.cpu.head(final)
         iso_w = self.cpu.head(final, order=1)
+        iso_x = self.cpu.head(final, order=3)
         lerr = float(np.max(np.abs(logits - iso["logits"])))
         head_gpu, head_wave = sp.rms_rel(logits, iso["logits"]), sp.rms_rel(iso_w["logits"], iso["logits"])
-        print(f"{label}: head max abs err {lerr:.2e}, RMS gpu {head_gpu:.3e} wave {head_wave:.3e}")
+        head_exact = sp.rms_rel(iso_x["logits"], iso["logits"])
+        print(f"{label}: head max abs err {lerr:.2e}, RMS gpu {head_gpu:.3e} wave {head_wave:.3e} "
+              f"exact-sum norm {head_exact:.3e}")
         assert lerr <= LOGIT_ABS, f"{label}: logits abs err {lerr}"
-        sp.check_layer_errors([head_gpu], [head_wave], label + " (head)", floor=HEAD_RMS_FLOOR)
+        sp.check_layer_errors([head_gpu], [max(head_wave, head_exact)], label + " (head)", floor=HEAD_RMS_FLOOR)
         # End to end against the serial run, within the oracle orders' spread.
         run = {"logits": logits, "hidden": hidden, "choices": out.choices}
         e2e, spread = sp.compare(run, ref), sp.compare(ref["wave"], ref)

@@ -434,6 +434,38 @@ def test_wave_square_sum_known_answer():
     assert np.array_equal(orc.rmsnorm_wave(xb, w, 1, 1024), orc.rmsnorm(xb, w, 1, 1024))
 
 
+def test_exact_square_sum_norm_known_answer_and_closed_form():
+    # The same row: serial order absorbs all 127 ones into 2^24 (sum 2^24),
+    # wave order keeps 126 of them, the exact sum keeps 127 and rounds once
+    # (2^24 + 127 is odd: FP32 keeps 2^24 + 128 by round-to-even of the ulp-2
+    # grid). Each sum gives its own inverse RMS, so the three outputs differ.
+    x = np.full(128, 0x3F80, np.uint16)
+    x[0] = 0x4580
+    w = np.full(128, 0x3F80, np.uint16)
+    inv = {}
+    for name, s in (("serial", 2.0 ** 24), ("wave", 2.0 ** 24 + 126), ("exact", 2.0 ** 24 + 128)):
+        ms = np.float32(np.float32(s) / np.float32(128))
+        inv[name] = np.float32(1.0) / np.float32(np.sqrt(np.float64(np.float32(ms + np.float32(1e-6)))))
+    want = {k: orc.f32_to_bf16((np.float32(4096.0) * v).astype(np.float32)) for k, v in inv.items()}
+    assert orc.rmsnorm_exact(x, w, 1, 128)[0] == want["exact"]
+    assert orc.rmsnorm(x, w, 1, 128)[0] == want["serial"]
+    assert orc.rmsnorm_wave(x, w, 1, 128)[0] == want["wave"]
+    # Closed form on random rows: the FP32 squares summed with math.fsum and
+    # rounded once, then the serial inverse and normalize-and-weight steps.
+    r = np.random.default_rng(11)
+    for width in (1024, 4096):
+        xb = orc.f32_to_bf16((r.standard_normal(width) * 30).astype(np.float32))
+        wb = orc.f32_to_bf16((r.standard_normal(width) + 1).astype(np.float32))
+        f = (xb.astype(np.uint32) << 16).view(np.float32)
+        total = np.float32(math.fsum(float(v) for v in (f * f).astype(np.float32)))
+        ms = np.float32(total / np.float32(width))
+        iv = np.float32(1.0) / np.float32(np.sqrt(np.float64(np.float32(ms + np.float32(1e-6)))))
+        xn = orc.f32_to_bf16((f * iv).astype(np.float32))
+        wf = (wb.astype(np.uint32) << 16).view(np.float32)
+        ref = orc.f32_to_bf16(((xn.astype(np.uint32) << 16).view(np.float32) * wf).astype(np.float32))
+        assert np.array_equal(orc.rmsnorm_exact(xb, wb, 1, width), ref), width
+
+
 def test_wave_attention_score_known_answer():
     # Two keys; key 0's dot is 2^24 + 1 - 2^24 with the terms in dims 0, 1, 64:
     # serial order absorbs the 1 (score 0, the zero-score mean 0x3f00 of
