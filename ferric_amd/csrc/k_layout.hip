@@ -150,13 +150,39 @@ __global__ void clear_word_kernel(uint32_t* word) {
 
 // System-scope loads read the coherent pinned buffer past every GPU cache, so
 // each step sees what the host wrote before the launch.
-__global__ __launch_bounds__(kThreads) void step_ingest_kernel(const uint32_t* __restrict__ host,
-                                                               uint32_t* __restrict__ dev, uint32_t words,
-                                                               uint32_t* err) {
-  if (blockIdx.x == 0 && threadIdx.x == 0 && err) *err = 0u;
+// The first launch of a decode step, one workgroup per row: each workgroup
+// copies its share of the step's metadata block (tokens, positions, page
+// tables) from coherent pinned host memory into device memory and gathers its
+// row's embedding, the token read from the host block itself (the device copy
+// is for the later launches). Workgroup 0 alone writes the step's error word:
+// it clears it and raises ERR_TOKEN if any row's token is out of range, so
+// the word has one writer in this launch (rows <= 64: one wave checks every
+// row's token). Out-of-range tokens read row 0.
+__global__ __launch_bounds__(kThreads) void step_embed_kernel(const uint32_t* __restrict__ host,
+                                                              uint32_t* __restrict__ dev, uint32_t words,
+                                                              const uint16_t* __restrict__ table,
+                                                              uint16_t* __restrict__ out, uint32_t rows,
+                                                              uint32_t hidden, uint32_t vocab, uint32_t* err) {
   uint32_t* src = const_cast<uint32_t*>(host);
-  for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < words; i += gridDim.x * kThreads)
+  const uint32_t row = blockIdx.x;
+  uint32_t tok = __hip_atomic_load(src + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  for (uint32_t i = row * kThreads + threadIdx.x; i < words; i += rows * kThreads)
     dev[i] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (row == 0 && threadIdx.x < 64) {
+    // Wave 0 of workgroup 0, lane r: row r's token (rows <= 64).
+    const bool bad =
+        threadIdx.x < rows && __hip_atomic_load(src + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) >= vocab;
+    const bool any = __ballot(bad) != 0ull;
+    if (threadIdx.x == 0 && err) *err = any ? (uint32_t)ERR_TOKEN : 0u;
+  }
+  if (tok >= vocab) tok = 0;
+  const uint32_t kb_count = hidden >> 5;
+  const uint32_t nb = tok >> 4, r = tok & 15u;
+  for (uint32_t c = threadIdx.x; c < hidden / 8; c += kThreads) {
+    uint32_t kb = c >> 2, g = c & 3u;
+    uint64_t s = ((((uint64_t)nb * kb_count + kb) * 64u) + r + 16u * g) << 3;
+    *reinterpret_cast<uint4*>(out + (uint64_t)row * hidden + c * 8) = *reinterpret_cast<const uint4*>(table + s);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void copy_u16_kernel(const uint16_t* __restrict__ src,
@@ -221,9 +247,12 @@ hipError_t launch_clear_word(uint32_t* word, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_step_ingest(const uint32_t* host, uint32_t* dev, uint32_t words, uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL(step_ingest_kernel, dim3(grid_for(words, kThreads, 256)), dim3(kThreads), 0, s, host, dev, words,
-                     err);
+hipError_t launch_step_embed(const uint32_t* host, uint32_t* dev, uint32_t words, const uint16_t* table_tiled,
+                             uint16_t* out, uint32_t rows, uint32_t hidden, uint32_t vocab, uint32_t* err,
+                             hipStream_t s) {
+  if (rows == 0 || rows > 64 || words < rows) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(step_embed_kernel, dim3(rows), dim3(kThreads), 0, s, host, dev, words, table_tiled, out, rows,
+                     hidden, vocab, err);
   return hipGetLastError();
 }
 

@@ -85,10 +85,14 @@ hipError_t launch_kv_fill(uint16_t* cache, const uint32_t* table, const uint32_t
 hipError_t launch_gather_rows(const uint16_t* src, const uint32_t* index, uint16_t* dst, uint32_t rows,
                               uint32_t width, hipStream_t s);
 hipError_t launch_clear_word(uint32_t* word, hipStream_t s);
-// The first launch of a decode step: copies `words` 32-bit words of step
-// metadata from coherent pinned host memory to device memory and clears the
-// error word, in place of a host-to-device copy and a clear.
-hipError_t launch_step_ingest(const uint32_t* host, uint32_t* dev, uint32_t words, uint32_t* err, hipStream_t s);
+// The first launch of a decode step (one workgroup per row): copies `words`
+// 32-bit words of step metadata from coherent pinned host memory to device
+// memory (in place of a host-to-device copy), sets the error word to 0 or
+// ERR_TOKEN, and writes each row's embedding ([rows][hidden] row-major) for
+// the token at host[row] (the block starts with the rows' tokens).
+hipError_t launch_step_embed(const uint32_t* host, uint32_t* dev, uint32_t words, const uint16_t* table_tiled,
+                             uint16_t* out, uint32_t rows, uint32_t hidden, uint32_t vocab, uint32_t* err,
+                             hipStream_t s);
 hipError_t launch_copy_u16(const uint16_t* src, uint16_t* dst, uint64_t count, hipStream_t s);
 
 // norms / activation

@@ -3,8 +3,8 @@
 // replacement for EngineeringTpBatchExecutionV2::forward
 // (adapters/m1-engineering-execution-v1/src/tp_execution/batched.rs:1746-2454).
 //
-// One decode step = 6 + (7, 8 or 9) x layers kernel launches (one row:
-// 5 + (5, 6 or 7) x layers, the norms inside the projections) on one HIP
+// One decode step = 5 + (7, 8 or 9) x layers kernel launches (one row:
+// 4 + (5, 6 or 7) x layers, the norms inside the projections) on one HIP
 // stream (enqueue_step; fh_expected_dispatch_count counts the same code
 // without launching), optionally replayed from a HIP graph captured once per
 // row count and attention form. All per-step inputs
@@ -455,7 +455,6 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
   const uint32_t H = md.hidden, QH = md.query_heads, KVH = md.kv_heads, Q = QH * 128, I = md.intermediate;
   const uint32_t cap = op.row_capacity, stride = op.page_table_stride, P = op.physical_pages,
                  C = op.context_tokens;
-  const uint32_t* d_tok = ctx->d_meta;
   const uint32_t* d_pos = ctx->d_meta + cap;
   const uint32_t* d_tab = ctx->d_meta + 2 * cap;
   uint32_t* err = ctx->err;
@@ -478,8 +477,10 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
   // The step's tokens, positions and page tables come in from the pinned
   // host mirror by the first launch, so a replayed graph needs no copy beside it.
   const uint32_t meta_words = 2 * cap + R * stride;
-  L(FH_KC_EMBEDDING, [&] { return fh::launch_step_ingest(ctx->h_meta, ctx->d_meta, meta_words, err, s); });
-  L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, ctx->hidden, R, H, md.vocabulary, err, s); });
+  L(FH_KC_EMBEDDING, [&] {
+    return fh::launch_step_embed(ctx->h_meta, ctx->d_meta, meta_words, ctx->embed, ctx->hidden, R, H, md.vocabulary,
+                                 err, s);
+  });
   // One row: each residual + RMSNorm runs in the prologue of the projection
   // that consumes the normalized row (QKV, gate/up, LM head), so a layer is 5
   // launches. Every workgroup of that projection reads the residual row and

@@ -26,14 +26,14 @@ L06 = ferric_amd.QWEN3_0_6B["layers"]
 
 
 def decode_launches(layers, qk_in_attention, merge_in_attention, capture=False, one_row=False):
-    """Launches of a decode step: step ingest, embedding; per layer RMSNorm,
+    """Launches of a decode step: metadata ingest + embedding; per layer RMSNorm,
     QKV, [QK-norm/RoPE/KV append], attention partitions, [merge], O, RMSNorm,
     gate/up, down; final norm, head, two argmax passes; one copy per layer
     when the residual stream is captured. One row: the three norms run inside
     the QKV, gate/up and head launches."""
     per_layer = 7 + (0 if qk_in_attention else 1) + (0 if merge_in_attention else 1)
     norms = 2 * layers + 1 if one_row else 0
-    return 6 + layers * per_layer + (layers if capture else 0) - norms
+    return 5 + layers * per_layer + (layers if capture else 0) - norms
 
 
 def prefill_launches(layers, rows, outputs):
@@ -85,7 +85,7 @@ def test_8b_decode_graph_keys_in_turn(runner8b):
     b32 = decode_launches(L8, False, False)
     # One row: both inside the attention launch, the norms inside the projections.
     b1 = decode_launches(L8, True, True, one_row=True)
-    assert (b32, b1) == (330, 185)
+    assert (b32, b1) == (329, 184)
     for step in range(3):
         # Capture, replay, and replays of the other graph key in between.
         run_checked(runner, pool, rows32(10 * step), expect=b32)
@@ -137,13 +137,13 @@ def test_0_6b_batch32_and_capture():
             # partitions > 1024, so the merge has its own launch.
             expect = decode_launches(L06, True, False, capture=capture)
             if not capture:
-                assert expect == 230
+                assert expect == 229
             for step in range(2):
                 run_checked(runner, pool, [(s, 3 + step) for s in sids], expect=expect)
             # One row: the norms inside the QKV, gate/up and head launches; the
             # capture copies read the residual stream's current buffer.
             one = decode_launches(L06, True, True, capture=capture, one_row=True)
-            assert one == (145 + 28 if capture else 145)
+            assert one == (144 + 28 if capture else 144)
             for step in range(2):
                 run_checked(runner, pool, [(sids[0], 5 + step)], expect=one)
         finally:
