@@ -150,38 +150,51 @@ __global__ void clear_word_kernel(uint32_t* word) {
 
 // System-scope loads read the coherent pinned buffer past every GPU cache, so
 // each step sees what the host wrote before the launch.
-// The first launch of a decode step, one workgroup per row: each workgroup
-// copies its share of the step's metadata block (tokens, positions, page
-// tables) from coherent pinned host memory into device memory and gathers its
-// row's embedding, the token read from the host block itself (the device copy
-// is for the later launches). Workgroup 0 alone writes the step's error word:
-// it clears it and raises ERR_TOKEN if any row's token is out of range, so
-// the word has one writer in this launch (rows <= 64: one wave checks every
-// row's token). Out-of-range tokens read row 0.
+// The first launch of a decode step. The metadata block (tokens, positions,
+// page tables) comes in from coherent pinned host memory, one word per thread
+// over the whole grid; workgroup r < rows also gathers row r's embedding, its
+// token read once from the host block itself (the device copy is for the
+// later launches). Workgroup 0 alone writes the step's error word: it clears
+// it and raises ERR_TOKEN if any row's token is out of range (rows <= 64: one
+// wave checks every row's token), so the word has one writer in this launch.
+// Out-of-range tokens read row 0.
 __global__ __launch_bounds__(kThreads) void step_embed_kernel(const uint32_t* __restrict__ host,
                                                               uint32_t* __restrict__ dev, uint32_t words,
                                                               const uint16_t* __restrict__ table,
                                                               uint16_t* __restrict__ out, uint32_t rows,
                                                               uint32_t hidden, uint32_t vocab, uint32_t* err) {
+  __shared__ uint32_t tok_s;
   uint32_t* src = const_cast<uint32_t*>(host);
-  const uint32_t row = blockIdx.x;
-  uint32_t tok = __hip_atomic_load(src + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  for (uint32_t i = row * kThreads + threadIdx.x; i < words; i += rows * kThreads)
+  const uint32_t blk = blockIdx.x;
+  // The first word of this thread's share, this row's token and (wave 0 of
+  // workgroup 0) the rows' tokens for the check are requested together: one
+  // round trip over the host link instead of one after another.
+  const uint32_t i0 = blk * kThreads + threadIdx.x;
+  const uint32_t w0 = i0 < words ? __hip_atomic_load(src + i0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : 0u;
+  const uint32_t t0 =
+      blk < rows && threadIdx.x == 0 ? __hip_atomic_load(src + blk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : 0u;
+  const uint32_t tc = blk == 0 && threadIdx.x < rows
+                          ? __hip_atomic_load(src + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                          : 0u;
+  if (i0 < words) dev[i0] = w0;
+  for (uint32_t i = i0 + gridDim.x * kThreads; i < words; i += gridDim.x * kThreads)
     dev[i] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  if (row == 0 && threadIdx.x < 64) {
-    // Wave 0 of workgroup 0, lane r: row r's token (rows <= 64).
-    const bool bad =
-        threadIdx.x < rows && __hip_atomic_load(src + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) >= vocab;
-    const bool any = __ballot(bad) != 0ull;
+  if (blk == 0 && threadIdx.x < 64) {
+    // Wave 0 of workgroup 0, lane r: row r's token.
+    const bool any = __ballot(threadIdx.x < rows && tc >= vocab) != 0ull;
     if (threadIdx.x == 0 && err) *err = any ? (uint32_t)ERR_TOKEN : 0u;
   }
+  if (blk >= rows) return;  // uniform per workgroup
+  if (threadIdx.x == 0) tok_s = t0;
+  __syncthreads();
+  uint32_t tok = tok_s;
   if (tok >= vocab) tok = 0;
   const uint32_t kb_count = hidden >> 5;
   const uint32_t nb = tok >> 4, r = tok & 15u;
   for (uint32_t c = threadIdx.x; c < hidden / 8; c += kThreads) {
     uint32_t kb = c >> 2, g = c & 3u;
-    uint64_t s = ((((uint64_t)nb * kb_count + kb) * 64u) + r + 16u * g) << 3;
-    *reinterpret_cast<uint4*>(out + (uint64_t)row * hidden + c * 8) = *reinterpret_cast<const uint4*>(table + s);
+    uint64_t sidx = ((((uint64_t)nb * kb_count + kb) * 64u) + r + 16u * g) << 3;
+    *reinterpret_cast<uint4*>(out + (uint64_t)blk * hidden + c * 8) = *reinterpret_cast<const uint4*>(table + sidx);
   }
 }
 
@@ -251,7 +264,8 @@ hipError_t launch_step_embed(const uint32_t* host, uint32_t* dev, uint32_t words
                              uint16_t* out, uint32_t rows, uint32_t hidden, uint32_t vocab, uint32_t* err,
                              hipStream_t s) {
   if (rows == 0 || rows > 64 || words < rows) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(step_embed_kernel, dim3(rows), dim3(kThreads), 0, s, host, dev, words, table_tiled, out, rows,
+  const uint32_t grid = std::max<uint32_t>(rows, grid_for(words, kThreads, 256));
+  hipLaunchKernelGGL(step_embed_kernel, dim3(grid), dim3(kThreads), 0, s, host, dev, words, table_tiled, out, rows,
                      hidden, vocab, err);
   return hipGetLastError();
 }
