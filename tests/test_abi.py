@@ -217,19 +217,35 @@ def test_page_pool_large_batch_matches_row_loop():
         rows = [(sids[i], int(t)) for i, t in zip(rng.integers(0, 5, 600), rng.integers(0, 151936, 600))]
         return pool, rows
 
-    # A decode step (every row a different sequence) takes the per-column path.
+    # A decode step (every row a different sequence) takes the per-column path,
+    # which reuses the previous decode batch's page-list block while the
+    # sequences and their page counts are unchanged: 40 steps in a row (page
+    # boundaries crossed, a sequence released and another admitted) against
+    # the row loop on a twin pool.
     for pick in ([0, 1, 2, 3, 4], [4, 2, 0, 3, 1]):
         pool_a, _ = build()
         pool_b, _ = build()
         sa, sb = sorted(pool_a.sequences), sorted(pool_b.sequences)
-        ca = pool_a._prepare_distinct([(sa[i], 100 + i) for i in pick])
-        cb = pool_b._prepare_loop([(sb[i], 100 + i) for i in pick])
-        assert [st.sequence for st in ca[0]] == [st.sequence for st in cb[0]]
-        for x, y in zip(ca[1:], cb[1:]):
-            np.testing.assert_array_equal(x, y)
-        assert pool_a.free == pool_b.free
+        for step in range(40):
+            if step == 20:
+                pool_a.release(sa[pick[1]])
+                pool_b.release(sb[pick[1]])
+                sa[pick[1]], sb[pick[1]] = pool_a.admit(3), pool_b.admit(3)
+            ba = pool_a._prepare_decode([(sa[i], 100 + step + i) for i in pick])
+            states, sid, token, pos, group = pool_b._prepare_loop([(sb[i], 100 + step + i) for i in pick])
+            rows = ba.rows
+            np.testing.assert_array_equal(rows.token, token)
+            np.testing.assert_array_equal(rows.position, pos)
+            for i, r in enumerate(rows):
+                np.testing.assert_array_equal(r.physical_pages, states[group[i]].pages)
+                assert r.writable_physical_page == r.physical_pages[r.position // 16]
+                assert not r.physical_pages.flags.writeable
+            assert pool_a.free == pool_b.free
+            pool_a.commit(ba)
+            for s, p in zip(sid.tolist(), pos.tolist()):
+                pool_b.sequences[s].length = p + 1
     pool_a, _ = build()
-    assert pool_a._prepare_distinct([(1, 5), (2, 6), (1, 7)]) is None  # a repeated sequence
+    assert pool_a._prepare_decode([(1, 5), (2, 6), (1, 7)]) is None  # a repeated sequence
     pool_a, rows = build()
     pool_b, _ = build()
     cols_a = pool_a._prepare_vector(rows)
