@@ -730,6 +730,8 @@ class ParityRunner:
         if outs:
             outs = list(outs)
             logits = pair.gpu.read_logits()
+            if len(batch.rows) <= pair.gpu.row_capacity():
+                logits = logits[outs]  # a decode batch keeps every row's logits, in row order
             ref_l, wave_l = ref["logits"][outs], wave["logits"][outs]
             e2e = float(np.max(np.abs(logits - ref_l)))
             spread = float(np.max(np.abs(wave_l - ref_l)))
@@ -758,9 +760,14 @@ SPEC_SHAPES = {
     # target (untied head) and a 0.6B-shaped draft (tied head), 32
     # sequences, so every verify is a 160-row batch
     "8b-target-0.6b-draft": (dict(ferric_amd.QWEN3_8B, layers=2), dict(ferric_amd.QWEN3_0_6B, layers=2), False, 32, 2),
+    # the same pair at full depth (36 + 28 layers): 4 sequences, so every
+    # verify is a 20-row chunk of the prefill path, every batch of both models
+    # against the oracle
+    "8b-0.6b-full-depth": (dict(ferric_amd.QWEN3_8B), dict(ferric_amd.QWEN3_0_6B), False, 4, 2),
 }
 
 
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("shape", list(SPEC_SHAPES))
 def test_speculative_rounds_match_the_oracle(shape):
     # Greedy speculation (K = 4), every draft step, catch-up and verify batch
