@@ -166,10 +166,22 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t p0 = split * PP;
 
+  // This wave's pages: [w0, w0 + np) of the row. The page-table entries are
+  // requested together with the position (they do not depend on it), so the
+  // K loads wait for one memory round trip, not two.
+  const uint32_t w0 = p0 + wave * kWavePages;
+  const uint32_t* trow = table + (uint64_t)r * stride;
+  static_assert(kWavePages <= 64, "one page-table entry per lane");
+  const uint32_t raw_phys = lane < (int)kWavePages && w0 + lane < stride ? trow[w0 + lane] : 0u;
+  const uint32_t pos = positions[r];
+  __builtin_amdgcn_sched_barrier(0);
+
   // Fused QK-norm, part 1. Wave w < G forms query head h G + w, wave G the
   // key head and wave G + 1 the value head of KV head h (lane l: elements l
-  // and l + 64). Their slab and norm-weight loads go out first: a wave's
-  // loads complete in issue order, so anything requested after the K loads
+  // and l + 64). Their slab and norm-weight loads go out right after the
+  // position and page-table loads and before the K loads: a wave's loads
+  // complete in issue order, so the K addresses (which need the position)
+  // do not wait for the slabs, and anything requested after the K loads
   // could only be used once K has landed.
   const int qk_role = kQkn && wave < G + 2 ? wave : -1;
   float qk_a[kQkn ? QKS : 1], qk_b[kQkn ? QKS : 1];
@@ -193,14 +205,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_partition_kernel(
     qk_wb = wn[lane + 64];
   }
   __builtin_amdgcn_sched_barrier(0);
-  // This wave's pages: [w0, w0 + np) of the row. The page-table entries are
-  // requested together with the position (they do not depend on it), so the
-  // K loads wait for one memory round trip, not two.
-  const uint32_t w0 = p0 + wave * kWavePages;
-  const uint32_t* trow = table + (uint64_t)r * stride;
-  static_assert(kWavePages <= 64, "one page-table entry per lane");
-  const uint32_t raw_phys = lane < (int)kWavePages && w0 + lane < stride ? trow[w0 + lane] : 0u;
-  const uint32_t pos = positions[r];
   if (pos >= context || pos / 16 >= stride) {
     // (The separate QK-norm kernel reports this row's missing KV slot as a
     // page fault; the fused form reports both.)
