@@ -184,9 +184,10 @@ __global__ __launch_bounds__(kHeadsPerGroup * 64) void qknorm_rope_kv_kernel(
 }
 
 // Residual + RMSNorm (see fh_op_residual_rmsnorm): one workgroup per row,
-// 16-byte chunks c = tid, tid + 256, ... of the row. S as in the QK-norm
-// kernel: 0 = no partials, > 0 = compile-time split count, < 0 = any count.
-template <int S>
+// 16-byte chunks c = tid, tid + 256, ... of the row (CH of them per thread,
+// width <= CH * 2048). S as in the QK-norm kernel: 0 = no partials, > 0 =
+// compile-time split count, < 0 = any count.
+template <int S, int CH>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t* __restrict__ hidden,
                                                                         const float* __restrict__ part,
                                                                         uint32_t splits,
@@ -198,35 +199,60 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
   const uint32_t row = blockIdx.x;
   uint16_t* hr = hidden + (uint64_t)row * width;
   const uint32_t chunks = width / 8;
-  constexpr int kMaxPerThread = 4;  // width <= 8192
   const uint64_t slab = (uint64_t)slab_rows * width;
-  uint4 v[kMaxPerThread], wv[kMaxPerThread];
+  const uint64_t slab4 = slab / 4;
+  // With a compile-time split count every chunk's row and slab loads are
+  // issued before the first fold (one memory round trip for the whole row)
+  // while the slab registers stay within 128 VGPRs; the arithmetic and its
+  // order are the same either way.
+  constexpr bool kLoadsFirst = S > 0 && CH * S <= 16;
+  uint4 v[CH], wv[CH];
+  float4 pre[kLoadsFirst ? CH : 1][kLoadsFirst ? S : 1][2];
   float sum = 0.f;
   bool bad = false;
   // The norm weight is loaded with the row, not after the reduction: one
   // memory round trip less on this latency-bound kernel.
 #pragma unroll
-  for (int j = 0; j < kMaxPerThread; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const uint32_t c = threadIdx.x + j * kNormThreads;
     if (c < chunks) wv[j] = *reinterpret_cast<const uint4*>(w + c * 8);
   }
+  if constexpr (kLoadsFirst) {
 #pragma unroll
-  for (int j = 0; j < kMaxPerThread; ++j) {
+    for (int j = 0; j < CH; ++j) {
+      const uint32_t c = threadIdx.x + j * kNormThreads;
+      if (c < chunks) {
+        v[j] = *reinterpret_cast<const uint4*>(hr + c * 8);
+        const float4* pr = reinterpret_cast<const float4*>(part + (uint64_t)row * width + c * 8);
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) {
+          pre[j][sp][0] = pr[sp * slab4];
+          pre[j][sp][1] = pr[sp * slab4 + 1];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
     const uint32_t c = threadIdx.x + j * kNormThreads;
     if (c < chunks) {
-      v[j] = *reinterpret_cast<const uint4*>(hr + c * 8);
+      if constexpr (!kLoadsFirst) v[j] = *reinterpret_cast<const uint4*>(hr + c * 8);
       if constexpr (S != 0) {
         // h = bf16((0 + (P_0 + P_1 + ...)) + h), v5 collective.rs:25-60 with
         // the split-K slabs added in split order.
         const float4* pr = reinterpret_cast<const float4*>(part + (uint64_t)row * width + c * 8);
-        const uint64_t slab4 = slab / 4;
         float a[8];
         if constexpr (S > 0) {
           float4 p[S][2];
 #pragma unroll
           for (int sp = 0; sp < S; ++sp) {
-            p[sp][0] = pr[sp * slab4];
-            p[sp][1] = pr[sp * slab4 + 1];
+            if constexpr (kLoadsFirst) {
+              p[sp][0] = pre[j][sp][0];
+              p[sp][1] = pre[j][sp][1];
+            } else {
+              p[sp][0] = pr[sp * slab4];
+              p[sp][1] = pr[sp * slab4 + 1];
+            }
           }
           a[0] = p[0][0].x; a[1] = p[0][0].y; a[2] = p[0][0].z; a[3] = p[0][0].w;
           a[4] = p[0][1].x; a[5] = p[0][1].y; a[6] = p[0][1].z; a[7] = p[0][1].w;
@@ -267,7 +293,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(uint16_t
   const float inv = inverse_rms(total, (float)width, eps);
   if (!is_finite_f32(total) || !is_finite_f32(inv)) bad = true;
 #pragma unroll
-  for (int j = 0; j < kMaxPerThread; ++j) {
+  for (int j = 0; j < CH; ++j) {
     const uint32_t c = threadIdx.x + j * kNormThreads;
     if (c < chunks) {
       const uint32_t xs[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
@@ -476,9 +502,17 @@ hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint
                        hidden, w, y, rows, act_mtiles(rows), width, eps, err);
     return hipGetLastError();
   }
-#define FH_RESNORM(S_)                                                                                             \
-  hipLaunchKernelGGL(residual_rmsnorm_kernel<S_>, dim3(rows), dim3(kNormThreads), 0, s, hidden, partials, splits, w, \
-                     y, y_tiled ? act_mtiles(rows) : 0u, width, eps, partial_slab_rows(rows), err)
+  const uint32_t per_thread = (width / 8 + kNormThreads - 1) / kNormThreads;  // 16-byte chunks
+#define FH_RESNORM_CH(S_, CH_)                                                                                     \
+  hipLaunchKernelGGL((residual_rmsnorm_kernel<S_, CH_>), dim3(rows), dim3(kNormThreads), 0, s, hidden, partials,  \
+                     splits, w, y, y_tiled ? act_mtiles(rows) : 0u, width, eps, partial_slab_rows(rows), err)
+#define FH_RESNORM(S_)                   \
+  if (per_thread <= 1)                   \
+    FH_RESNORM_CH(S_, 1);                \
+  else if (per_thread <= 2)              \
+    FH_RESNORM_CH(S_, 2);                \
+  else                                   \
+    FH_RESNORM_CH(S_, 4)
   switch (partials ? splits : 0) {
     case 0: FH_RESNORM(0); break;
     case 1: FH_RESNORM(1); break;
@@ -490,6 +524,7 @@ hipError_t launch_residual_rmsnorm(uint16_t* hidden, const float* partials, uint
     default: FH_RESNORM(-1); break;
   }
 #undef FH_RESNORM
+#undef FH_RESNORM_CH
   return hipGetLastError();
 }
 
