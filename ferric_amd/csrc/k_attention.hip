@@ -95,10 +95,47 @@ __device__ __forceinline__ float load_record(const float* p) {
 
 // COHERENT: every record load is an agent-scope atomic load (records written
 // in the same launch by workgroups on other XCDs, see the partition kernel).
+constexpr uint32_t kMergeInFlight = 16;
 template <bool COHERENT = false>
 __device__ __forceinline__ void merge_records(const float* p, uint32_t ns, int lane, float& L, float& n0,
                                               float& n1) {
   const float kNegInf = -__builtin_inff();
+  if (ns <= kMergeInFlight) {
+    // Up to 16 partitions: every record's m and l (lane s: partition s) and
+    // this lane's two numerators of every record are requested at once, one
+    // memory round trip; then the arithmetic below in the same order. The
+    // loads are unconditional (indices past the last record re-read it) so
+    // that none sits in a branch whose join would wait for it.
+    const bool own = (uint32_t)lane < ns;
+    const float* pl = p + (uint64_t)min((uint32_t)lane, ns - 1) * kAttnPartialFloats;
+    const float m_raw = load_record<COHERENT>(pl);
+    const float l_raw = load_record<COHERENT>(pl + 1);
+    float a0[kMergeInFlight], a1[kMergeInFlight];
+#pragma unroll
+    for (uint32_t u = 0; u < kMergeInFlight; ++u) {
+      const float* ps = p + (uint64_t)min(u, ns - 1) * kAttnPartialFloats;
+      a0[u] = load_record<COHERENT>(ps + 2 + 2 * lane);
+      a1[u] = load_record<COHERENT>(ps + 3 + 2 * lane);
+    }
+    const float ms = own ? m_raw : kNegInf;
+    const float ls = own ? l_raw : 0.f;
+    const float M = wave_max(ms);
+    const float ws = own ? expf(ms - M) : 0.f;
+    const float lw = own ? ls * ws : 0.f;
+    L = 0.f;
+    n0 = 0.f;
+    n1 = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < kMergeInFlight; ++u) {
+      if (u < ns) {
+        const float w = lane_bcast(ws, (int)u);
+        L += lane_bcast(lw, (int)u);
+        n0 += a0[u] * w;
+        n1 += a1[u] * w;
+      }
+    }
+    return;
+  }
   float mloc = kNegInf;
   for (uint32_t sp = lane; sp < ns; sp += 64) mloc = fmaxf(mloc, load_record<COHERENT>(p + (uint64_t)sp * kAttnPartialFloats));
   const float M = wave_max(mloc);
