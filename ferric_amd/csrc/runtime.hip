@@ -1144,6 +1144,11 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
     i = j;
   }
+  // Longest first: a block reads the pages up to its last row's position, and
+  // workgroups are dispatched in block order, so the short ones fill the tail.
+  std::stable_sort(blocks, blocks + nblocks, [&](uint32_t a, uint32_t b) {
+    return rows[(a & 0xffffu) + (a >> 16) - 1].position > rows[(b & 0xffffu) + (b >> 16) - 1].position;
+  });
   auto poison = [&](fh_status s2, const std::string& msg) {
     ctx->poisoned = true;
     return fail(ctx, s2, msg);
