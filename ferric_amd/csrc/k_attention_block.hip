@@ -10,10 +10,15 @@
 // host groups such a run into blocks of up to 64 / G rows and this kernel
 // reads each K/V page once per block instead of once per row.
 //
-// Grid (block, KV head), 4 waves. A wave owns 16 query vectors: 16 / G rows
-// times the G query heads of the KV head (vector j: row j / G, head j % G).
-// Per 16-token page, shared by the workgroup through LDS (double-buffered,
-// the next page's loads in flight while this one is used):
+// Grid (block, KV head), 4 waves per page phase. A wave owns 16 query
+// vectors: 16 / G rows times the G query heads of the KV head (vector j: row
+// j / G, head j % G). With PH page phases (PH groups of 4 waves, for grids
+// too small to give every SIMD more than one wave, such as a speculative
+// verify's few short blocks), phase f walks pages f, f + PH, f + 2 PH, ...
+// and the phases' softmax states are folded pairwise through LDS at the end
+// (m = max, the other terms scaled by exp(m_f - m)). Per 16-token page,
+// shared by the phase's 4 waves through LDS (double-buffered, the next
+// page's loads in flight while this one is used):
 //   S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (K page re-laid through a padded
 //   LDS tile into the A operand, the queries as the B operand), scaled and
 //   masked by each row's position (t <= p);
@@ -47,31 +52,58 @@ __device__ __forceinline__ float exp2_based(float x) { return __builtin_amdgcn_e
 // a pad) spread a wave's 64 stores over 16 banks.
 constexpr int kVtPitch = 9;
 
-template <int G>
-__global__ __launch_bounds__(256, 4) void attn_block_kernel(
+// LDS of a workgroup: per phase a double-buffered K tile and V tile; after
+// the page loop the same bytes hold the phase states being folded, one slot
+// per (phase pair, row group): 8 accumulator tiles of 64 lanes, then m and l
+// of 16 vectors.
+template <int PH>
+struct BlockLds {
+  static constexpr size_t kK = sizeof(u32x4) * PH * 2 * 16 * 17;
+  static constexpr size_t kV = sizeof(uint32_t) * PH * 2 * 128 * kVtPitch;
+  static constexpr size_t kSlot = sizeof(f32x4) * 8 * 64 + 2 * 16 * sizeof(float);
+  static constexpr size_t kStage = PH > 1 ? (PH / 2) * 4 * kSlot : 0;
+  static constexpr size_t kBytes = kK + kV > kStage ? kK + kV : kStage;
+};
+
+template <int G, int PH>
+__global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, const uint32_t* __restrict__ blocks,
     uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
     uint32_t context, uint32_t* err) {
   constexpr int kRowsPerWave = 16 / G;
   static_assert(16 % G == 0, "16 query vectors per wave");
+  static_assert(PH == 1 || PH == 2 || PH == 4, "page phases");
   const uint32_t desc = blocks[blockIdx.x];
   const uint32_t row0 = desc & 0xffffu, nrows = desc >> 16;
   const uint32_t h = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = PH == 1 ? w : w & 3, phase = PH == 1 ? 0 : w >> 2;  // row group within the phase, page phase
   const uint32_t last = row0 + nrows - 1;
-  const uint32_t pmax = positions[last];  // rows of a block have consecutive positions
-  if (pmax >= context || pmax / 16 >= stride) {
-    if (h == 0 && threadIdx.x == 0) raise_error(err, ERR_POSITION);
-    return;
-  }
-  const uint32_t npages = pmax / 16 + 1;
   const uint32_t* trow = table + (uint64_t)last * stride;
+  // The phase's first three page-table entries are requested with the
+  // position (entries past the sequence's pages are checked once npages is
+  // known), so the first K/V loads wait for one round trip, not two.
+  uint32_t tpre[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) tpre[i] = trow[min((uint32_t)(phase + i * PH), stride - 1)];
+  // Rows of a block have consecutive positions. A position past the context
+  // or the page table is reported and the block reads page 0 only, with no
+  // branch that the table loads above would be moved behind.
+  const uint32_t pos_last = positions[last];
+  const bool pos_ok = pos_last < context && pos_last / 16 < stride;
+  if (!pos_ok && h == 0 && threadIdx.x == 0) raise_error(err, ERR_POSITION);
+  const uint32_t pmax = pos_ok ? pos_last : 0u;
+  const uint32_t npages = pmax / 16 + 1;
 
-  __shared__ u32x4 ktile[2][16][17];
-  __shared__ uint32_t vtile[2][128][kVtPitch];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[BlockLds<PH>::kBytes];
+  auto ktile = reinterpret_cast<u32x4(*)[16][17]>(lds_raw + BlockLds<PH>::kK / PH * phase);
+  auto vtile = reinterpret_cast<uint32_t(*)[128][kVtPitch]>(lds_raw + BlockLds<PH>::kK + BlockLds<PH>::kV / PH * phase);
 
   const int j = lane & 15, g16 = lane >> 4;
+  // With page phases, a row group past the block's rows only helps load the
+  // pages (one phase runs the wave's arithmetic as it is: masked rows).
+  const bool live = PH == 1 || (uint32_t)(wave * kRowsPerWave) < nrows;
   const uint32_t rj = wave * kRowsPerWave + j / G;
   const bool qvalid = rj < nrows;
   const uint32_t qpos = qvalid ? positions[row0 + rj] : 0u;
@@ -86,27 +118,28 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
   }
 
   bool bad = false, bad_page = false;
-  auto phys = [&](uint32_t pi) {
-    uint32_t ph = pi < npages ? trow[pi] : 0u;
+  auto checked = [&](uint32_t pi, uint32_t ph) {
+    ph = pi < npages ? ph : 0u;
     if (ph >= pages) {
       bad_page = true;
       ph = 0;
     }
     return ph;
   };
+  auto phys = [&](uint32_t pi) { return checked(pi, pi < npages ? trow[pi] : 0u); };
   // K loader: thread t copies 16 bytes (dims 8 c .. 8 c + 7) of token t / 16.
   // V loader: wave w copies tokens 4 w .. 4 w + 3, one dword (dims 2 l,
   // 2 l + 1) per lane and token: a whole 256-byte row per load.
-  const uint32_t lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
+  const uint32_t lt = (threadIdx.x & 255) >> 4, lc = threadIdx.x & 15;
   auto ksrc = [&](uint32_t ph) { return (((uint64_t)ph * 16 + lt) * kvh + h) * 128 + 8 * lc; };
   auto vsrc = [&](uint32_t ph, int t) {
     return reinterpret_cast<const uint32_t*>(vc + (((uint64_t)ph * 16 + 4 * wave + t) * kvh + h) * 128) + lane;
   };
-  uint32_t ph_next = phys(1), ph_next2 = phys(2);
-  u32x4 kreg;
-  uint32_t vreg[4];
-  {
-    const uint32_t ph0 = phys(0);
+  uint32_t ph_next = checked(phase + PH, tpre[1]), ph_next2 = checked(phase + 2 * PH, tpre[2]);
+  u32x4 kreg = u32x4{0u, 0u, 0u, 0u};
+  uint32_t vreg[4] = {0u, 0u, 0u, 0u};
+  if (PH == 1 || (uint32_t)phase < npages) {
+    const uint32_t ph0 = checked(phase, tpre[0]);
     kreg = *reinterpret_cast<const u32x4*>(kc + ksrc(ph0));
 #pragma unroll
     for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph0, t);
@@ -126,30 +159,42 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
   // a NaN or infinity inside the PV MFMA would still poison the sum, so they
   // enter as zeros (the reference never reads past the row's position).
   const uint32_t last_slot = pmax % 16;
-  for (uint32_t p = 0; p < npages; ++p) {
-    const int b = p & 1;
-    ktile[b][lt][lc] = kreg;
-    if (p + 1 == npages) {
+  const uint32_t iters = (npages + PH - 1) / PH;
+  // One iteration: every phase's next page. Only the last iteration (LAST)
+  // can hold the block's last page or find a phase with no page left, and it
+  // issues no loads, so the loop before it runs without those branches.
+  auto step = [&](uint32_t it, auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const uint32_t p = phase + it * PH;
+    const bool here = !LAST || PH == 1 || p < npages;  // the phase has a page this iteration
+    const int b = it & 1;
+    if (here) {
+      ktile[b][lt][lc] = kreg;
+      if (LAST && p + 1 == npages) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if ((uint32_t)(4 * wave + t) > last_slot) vreg[t] = 0u;
-    }
-    // Tokens (4 w, 4 w + 1) and (4 w + 2, 4 w + 3) -> pairs 2 w and 2 w + 1,
-    // for dims 2 l (low halves) and 2 l + 1 (high halves).
+        for (int t = 0; t < 4; ++t)
+          if ((uint32_t)(4 * wave + t) > last_slot) vreg[t] = 0u;
+      }
+      // Tokens (4 w, 4 w + 1) and (4 w + 2, 4 w + 3) -> pairs 2 w and 2 w + 1,
+      // for dims 2 l (low halves) and 2 l + 1 (high halves).
 #pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-      const uint32_t t0 = vreg[2 * pr], t1 = vreg[2 * pr + 1];
-      vtile[b][2 * lane][2 * wave + pr] = (t0 & 0xffffu) | (t1 << 16);
-      vtile[b][2 * lane + 1][2 * wave + pr] = (t0 >> 16) | (t1 & 0xffff0000u);
-    }
-    if (p + 1 < npages) {
-      kreg = *reinterpret_cast<const u32x4*>(kc + ksrc(ph_next));
+      for (int pr = 0; pr < 2; ++pr) {
+        const uint32_t t0 = vreg[2 * pr], t1 = vreg[2 * pr + 1];
+        vtile[b][2 * lane][2 * wave + pr] = (t0 & 0xffffu) | (t1 << 16);
+        vtile[b][2 * lane + 1][2 * wave + pr] = (t0 >> 16) | (t1 & 0xffff0000u);
+      }
+      if (!LAST && (PH == 1 || p + PH < npages)) {
+        kreg = *reinterpret_cast<const u32x4*>(kc + ksrc(ph_next));
 #pragma unroll
-      for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph_next, t);
+        for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph_next, t);
+      }
     }
-    ph_next = ph_next2;
-    ph_next2 = phys(p + 3);
+    if (!LAST) {
+      ph_next = ph_next2;
+      ph_next2 = phys(p + 3 * PH);
+    }
     __syncthreads();
+    if (!here || !live) return;
 
     // Scores: lane l, element e holds key 4 g16 + e of the page for vector j.
     u32x4 ka[4];
@@ -207,6 +252,46 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
       acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_hi, vb, acc[d], 0, 0, 0);
       acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_lo, vb, acc[d], 0, 0, 0);
     }
+  };
+  for (uint32_t it = 0; it + 1 < iters; ++it) step(it, std::false_type{});
+  step(iters - 1, std::true_type{});
+
+  if constexpr (PH > 1) {
+    // Fold the phases pairwise: in the first round phase f + PH / 2 hands its
+    // state to phase f through slot f; in later rounds phase f + half hands
+    // it through slot f + half (which only that phase read before).
+    f32x4* st_acc = reinterpret_cast<f32x4*>(lds_raw);
+    float* st_ml = reinterpret_cast<float*>(lds_raw + sizeof(f32x4) * (PH / 2) * 4 * 8 * 64);
+    __syncthreads();  // every wave is done with the page tiles
+#pragma unroll
+    for (int half = PH / 2; half >= 1; half /= 2) {
+      const bool first = 2 * half == PH;
+      if (live && phase >= half && phase < 2 * half) {
+        const int slot = (first ? phase - half : phase) * 4 + wave;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) st_acc[(slot * 8 + d) * 64 + lane] = acc[d];
+        if (g16 == 0) {
+          st_ml[slot * 32 + j] = m_run;
+          st_ml[slot * 32 + 16 + j] = l_run;
+        }
+      }
+      __syncthreads();
+      if (live && phase < half) {
+        const int slot = (first ? phase : phase + half) * 4 + wave;
+        const float mo = st_ml[slot * 32 + j], lo = st_ml[slot * 32 + 16 + j];
+        const float m_new = fmaxf(m_run, mo);
+        const float a_self = m_run == kNegInf ? 0.f : exp2_based(m_run - m_new);
+        const float a_other = mo == kNegInf ? 0.f : exp2_based(mo - m_new);
+        l_run = l_run * a_self + lo * a_other;
+        m_run = m_new;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float fs = __shfl(a_self, 4 * g16 + e, 64), fo = __shfl(a_other, 4 * g16 + e, 64);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) acc[d][e] = acc[d][e] * fs + st_acc[(slot * 8 + d) * 64 + lane][e] * fo;
+        }
+      }
+    }
   }
 
 #pragma unroll
@@ -214,7 +299,7 @@ __global__ __launch_bounds__(256, 4) void attn_block_kernel(
     const int v = 4 * g16 + e;
     const float L = __shfl(l_run, v, 64);
     const uint32_t rv = wave * kRowsPerWave + v / G;
-    if (rv < nrows) {
+    if (phase == 0 && rv < nrows) {  // phase 0 holds the folded state
       bad |= !(L > 0.f);
       const uint32_t head = h * G + v % G;
 #pragma unroll
@@ -245,9 +330,20 @@ hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, c
   if (nblocks == 0) return hipSuccess;
   const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   const dim3 grid(nblocks, kvh);
-#define FH_BLOCKS(G_)                                                                                            \
-  hipLaunchKernelGGL(attn_block_kernel<G_>, grid, dim3(256), 0, s, q, k_cache, v_cache, positions, table, blocks, \
-                     out, mt, qh, kvh, stride, pages, context, err)
+  // Page phases so that a small grid still puts about four waves on each
+  // SIMD (256 CUs): a workgroup of 4 PH waves per block and head.
+  const uint64_t wgs = (uint64_t)nblocks * kvh;
+  const int ph = wgs <= 256 ? 4 : wgs <= 512 ? 2 : 1;
+#define FH_BLOCKS_PH(G_, PH_)                                                                                      \
+  hipLaunchKernelGGL((attn_block_kernel<G_, PH_>), grid, dim3(256 * PH_), 0, s, q, k_cache, v_cache, positions, \
+                     table, blocks, out, mt, qh, kvh, stride, pages, context, err)
+#define FH_BLOCKS(G_)                  \
+  if (ph == 4)                         \
+    FH_BLOCKS_PH(G_, 4);               \
+  else if (ph == 2)                    \
+    FH_BLOCKS_PH(G_, 2);               \
+  else                                 \
+    FH_BLOCKS_PH(G_, 1)
   switch (qh / kvh) {
     case 1: FH_BLOCKS(1); break;
     case 2: FH_BLOCKS(2); break;
@@ -256,6 +352,7 @@ hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, c
     default: return hipErrorInvalidValue;
   }
 #undef FH_BLOCKS
+#undef FH_BLOCKS_PH
   return hipGetLastError();
 }
 
