@@ -212,7 +212,7 @@ fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cac
     return FH_ERR_INVALID_ARGUMENT;
   const uint32_t g = query_heads / kv_heads;
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
-  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads, context_tokens);
   const uint64_t records = (uint64_t)rows * query_heads * fh::attn_max_splits(context_tokens, split_pages);
   if (records > kNoAllocAttnRecords) {
     fh::set_thread_error("fh_op_paged_attention_noalloc: rows x query_heads x partitions of the context exceeds "
@@ -234,7 +234,7 @@ fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cac
 
 uint64_t fh_attention_scratch_bytes(uint32_t rows, uint32_t query_heads, uint32_t context_tokens) {
   return (uint64_t)rows * query_heads *
-         fh::attn_max_splits(context_tokens, fh::attn_split_pages(rows, query_heads)) * fh::kAttnPartialFloats * 4;
+         fh::attn_max_splits(context_tokens, fh::attn_split_pages(rows, query_heads, context_tokens)) * fh::kAttnPartialFloats * 4;
 }
 
 fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_splits, const uint16_t* q_norm,
@@ -251,7 +251,7 @@ fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_s
     return FH_ERR_INVALID_ARGUMENT;
   hipStream_t s = as_stream(stream);
   float* part = reinterpret_cast<float*>(scratch);
-  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads, context_tokens);
   const fh::AttnQkn qa{qkv_partials, qkv_splits, fh::partial_slab_rows(rows), q_norm, k_norm, cos_table, sin_table,
                        k_cache,      v_cache,    epsilon};
   (void)hipGetLastError();
@@ -277,7 +277,7 @@ fh_status fh_op_paged_attention(const uint16_t* q, const uint16_t* k_cache, cons
   if (g != 1 && g != 2 && g != 4 && g != 8) return FH_ERR_INVALID_ARGUMENT;
   hipStream_t s = as_stream(stream);
   float* part = reinterpret_cast<float*>(scratch);
-  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads);
+  const uint32_t split_pages = fh::attn_split_pages(rows, query_heads, context_tokens);
   (void)hipGetLastError();
   hipError_t e = fh::launch_attention_partial(q, k_cache, v_cache, positions, page_table, part, out, out_tiled, 0,
                                               rows, rows, query_heads, kv_heads, stride, physical_pages,

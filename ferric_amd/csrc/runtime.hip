@@ -433,7 +433,7 @@ struct Enq {
 // requested after the scores there (occupancy kept at 3 workgroups per CU):
 // 32 rows 1.741-1.742 -> 1.733-1.734 ms device time per step.
 bool step_runs_qkn(const fh_ctx* ctx, uint32_t rows) {
-  const uint32_t split = fh::attn_split_pages(rows, ctx->md.query_heads);
+  const uint32_t split = fh::attn_split_pages(rows, ctx->md.query_heads, ctx->opt.context_tokens);
   return ctx->batch_private_slots &&
          fh::attention_qkn_supported(ctx->md.query_heads, ctx->md.kv_heads, ctx->s_qkv) &&
          (fh::attn_fuse_merge(rows, ctx->md.kv_heads, ctx->opt.context_tokens, split) ||
@@ -471,7 +471,7 @@ hipError_t enqueue_step(fh_ctx* ctx, uint32_t R, uint64_t* launches, bool dry = 
   // `hidden` (one rounding, as the TP1 residual); the QKV partials are folded
   // by the QK-norm kernel.
   const uint32_t sq = ctx->s_qkv, so = ctx->s_o, sd = ctx->s_down;
-  const uint32_t split = fh::attn_split_pages(R, QH);
+  const uint32_t split = fh::attn_split_pages(R, QH, C);
   const bool fuse = fh::attn_fuse_merge(R, KVH, C, split);
   const bool qkn = step_runs_qkn(ctx, R);
   // The step's tokens, positions and page tables come in from the pinned
@@ -1347,7 +1347,7 @@ fh_status fh_time_attention(fh_ctx* ctx, uint32_t reps, float* avg_ms) {
   const uint32_t* d_tab = ctx->d_meta + 2 * cap;
   hipStream_t s = ctx->stream;
   auto launch = [&] {
-    const uint32_t split = fh::attn_split_pages(R, md.query_heads);
+    const uint32_t split = fh::attn_split_pages(R, md.query_heads, op.context_tokens);
     const bool fuse = fh::attn_fuse_merge(R, md.kv_heads, op.context_tokens, split);
     // The attention kernel class of the step: the partition launch (with the
     // merge when the step fuses it; the merge launch is a class of its own).

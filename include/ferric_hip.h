@@ -342,9 +342,10 @@ fh_status fh_op_qknorm_paged_attention(const float* qkv_partials, uint32_t qkv_s
  * serving loops, harnesses that forbid hipMalloc). The partition records live in a
  * static device array of the library: 16384 records = 8.5 MB, held on every GPU the
  * library has launched on until the process ends. A launch needs rows x query_heads x
- * ceil(context_tokens / (16 x split_pages)) records, where split_pages is 16 (256-token
- * partitions) when rows x query_heads <= 64 or query_heads <= 16, else 32 (512-token
- * partitions); larger launches return FH_ERR_INVALID_ARGUMENT.
+ * ceil(context_tokens / (16 x split_pages)) records, where split_pages is 32 (512-token
+ * partitions) when 256 < context_tokens <= 512, else 16 (256-token partitions) when
+ * rows x query_heads <= 64 or query_heads <= 16, else 32; larger launches return
+ * FH_ERR_INVALID_ARGUMENT.
  * Calls that overlap on one GPU share that array and race. Same kernels and results
  * as fh_op_paged_attention. */
 fh_status fh_op_paged_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,

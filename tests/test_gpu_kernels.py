@@ -610,15 +610,19 @@ def test_qknorm_rope_kv_bit_exact(qh, kvh, splits, rows):
 
 
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (16, 8)])
-@pytest.mark.parametrize("tiled,many", [(0, False), (1, False), (1, True), (0, None)])
+@pytest.mark.parametrize("tiled,many", [(0, False), (1, False), (1, True), (0, None), (1, "short")])
 def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
     # Partition sizes follow the (rows x query heads) policy: 14 rows take
     # 32-page (qh 32) or 16-page (qh 16) partitions, 40 rows 32-page ones, and
-    # 2 rows 8-page ones (up to 65 partitions per row: more than one 64-lane
-    # chunk of partition weights in the merge).
-    r = rng(1000 + qh + 7 * bool(many) + 13 * (many is None))
+    # 2 rows 16-page ones (up to 33 partitions per row). A 512-token context
+    # ("short") takes one 32-page partition for every shape: each row ends in
+    # its partition, with no records and no merge.
+    r = rng(1000 + qh + 7 * bool(many) + 13 * (many is None) + 29 * (many == "short"))
     pages, stride, context = 600, 520, 8320
-    if many:
+    if many == "short":
+        context = 512
+        positions = np.array([0, 15, 16, 255, 256, 257, 300, 400, 500, 511, 100, 7, 480, 290], np.uint32)
+    elif many:
         # a prefill-size batch: 40 rows, tiled output of fh_activation_rows(40) rows
         positions = r.integers(0, 2000, 40).astype(np.uint32)
     elif many is None:
@@ -662,23 +666,25 @@ def test_paged_attention_within_tolerance(qh, kvh, tiled, many):
 # the 8B shape, one to 17 partitions), 16-page partitions (one 8B row at a
 # 4095-token context; 0.6B rows), pages of one and of several tokens, a
 # batch of 32 rows.
-@pytest.mark.parametrize("qh,kvh,positions", [
-    (32, 8, [0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 4190, 77, 3000, 2047]),
-    (32, 8, [4095]),
-    (16, 8, [0, 17, 300, 2047, 1500, 999, 16, 4000]),
-    (32, 8, "b32"),
-    (16, 8, "b32"),
+@pytest.mark.parametrize("qh,kvh,positions,context", [
+    (32, 8, [0, 15, 16, 255, 256, 511, 512, 513, 1000, 4095, 4190, 77, 3000, 2047], 4224),
+    (32, 8, [4095], 4224),
+    (16, 8, [0, 17, 300, 2047, 1500, 999, 16, 4000], 4224),
+    (32, 8, "b32", 4224),
+    (16, 8, "b32", 4224),
+    (16, 8, "b32", 512),
+    (32, 8, [0, 300, 511, 256, 257], 512),
 ])
-def test_qknorm_paged_attention_equals_the_two_launches(qh, kvh, positions):
+def test_qknorm_paged_attention_equals_the_two_launches(qh, kvh, positions, context):
     # The decode step's fused form (QK-norm + RoPE + KV append inside the
     # attention partitions) against fh_op_qknorm_rope_kv then
     # fh_op_paged_attention on the same split-K slabs: attention output, K and
     # V caches and the error word bit for bit. Each row writes a page no
     # other row lists (the fused form's contract).
-    r = rng(4242 + qh + (len(positions) if isinstance(positions, list) else 99))
-    pages, stride, context = 4096, 264, 4224
+    r = rng(4242 + qh + (len(positions) if isinstance(positions, list) else 99) + (context if context != 4224 else 0))
+    pages, stride = 4096, 264
     if positions == "b32":
-        positions = r.integers(0, 2048, 32)
+        positions = r.integers(0, min(2048, context), 32)
     positions = np.asarray(positions, np.uint32)
     rows = len(positions)
     per_row = pages // rows
