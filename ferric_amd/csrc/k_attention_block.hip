@@ -33,6 +33,14 @@
 //   through LDS transposed (dimension-major, two tokens per dword), so the B
 //   operand of a lane (keys 4 g .. 4 g + 3 of one dimension) is two dwords.
 // Finally out = bf16(n / l) for each valid row.
+//
+// QKN: the QK-norm, RoPE and KV append of the block's rows run here instead
+// of in the QK-norm kernel (used when no block reads a slot another block of
+// the chunk writes). The waves form the rows' G query heads, key head and
+// value head from the QKV projection's split-K slabs with the QK-norm
+// kernel's routine and order (bit-identical), keep them in LDS, write the key
+// and value into the rows' cache slots, and use the LDS copies wherever a
+// page holds one of those slots.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -65,13 +73,17 @@ struct BlockLds {
   static constexpr size_t kBytes = kK + kV > kStage ? kK + kV : kStage;
 };
 
-template <int G, int PH>
+// Split-K slabs the fused QK-norm folds at most (all requested at once).
+constexpr uint32_t kBlockQknMaxSplits = 8;
+
+template <int G, int PH, bool QKN>
 __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint32_t* __restrict__ positions, const uint32_t* __restrict__ table, const uint32_t* __restrict__ blocks,
     uint16_t* __restrict__ out, uint32_t out_mtiles, uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages,
-    uint32_t context, uint32_t* err) {
+    uint32_t context, uint32_t* err, AttnQkn qk) {
   constexpr int kRowsPerWave = 16 / G;
+  constexpr int kBlockRows = 64 / G;
   static_assert(16 % G == 0, "16 query vectors per wave");
   static_assert(PH == 1 || PH == 2 || PH == 4, "page phases");
   const uint32_t desc = blocks[blockIdx.x];
@@ -108,13 +120,15 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
   const bool qvalid = rj < nrows;
   const uint32_t qpos = qvalid ? positions[row0 + rj] : 0u;
   u32x4 qv[4];
-  if (qvalid) {
-    const uint16_t* qp = q + ((uint64_t)(row0 + rj) * qh + h * G + j % G) * 128 + 8 * g16;
+  if constexpr (!QKN) {
+    if (qvalid) {
+      const uint16_t* qp = q + ((uint64_t)(row0 + rj) * qh + h * G + j % G) * 128 + 8 * g16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
-  } else {
+      for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   bool bad = false, bad_page = false;
@@ -145,6 +159,106 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
     for (int t = 0; t < 4; ++t) vreg[t] = *vsrc(ph0, t);
   }
 
+  // Fused QK-norm (QKN): the block's rows' heads, formed while the first
+  // pages are in flight. Row i of the block holds position pos0 + i.
+  __shared__ __attribute__((aligned(16))) uint16_t qkn_q[QKN ? kBlockRows * G * 128 : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t qkn_k[QKN ? kBlockRows * 128 : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t qkn_v[QKN ? kBlockRows * 128 : 1];
+  uint32_t pos0 = 0;
+  if constexpr (QKN) {
+    pos0 = positions[row0];
+    const uint32_t ld = (qh + 2 * kvh) * 128;
+    const uint64_t slab = (uint64_t)qk.slab_rows * ld;
+    const uint32_t nwork = nrows * (G + 2);
+    // Each wave forms head-rows w, w + W, w + 2 W, ... (W waves), two at a
+    // time with every load of both in flight together. A head-row is (row i,
+    // role): roles 0..G-1 the query heads h G + role, G the key head and
+    // G + 1 the value head of KV head h.
+    constexpr uint32_t kWaves = 4 * PH;
+    for (uint32_t hr0 = w; hr0 < nwork; hr0 += 2 * kWaves) {
+      uint32_t hrs[2], rows_u[2], roles[2], pos[2];
+      float pa[2][kBlockQknMaxSplits], pb[2][kBlockQknMaxSplits];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        hrs[u] = min(hr0 + u * kWaves, nwork - 1);  // a second past the end re-reads the last (not stored)
+        const uint32_t i = hrs[u] / (G + 2);
+        roles[u] = hrs[u] % (G + 2);
+        rows_u[u] = row0 + i;
+        pos[u] = positions[rows_u[u]];
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t role = roles[u];
+        const uint32_t head = role < (uint32_t)G ? h * G + role : (role == (uint32_t)G ? qh + h : qh + kvh + h);
+        const float* pp = qk.qkv_part + (uint64_t)rows_u[u] * ld + head * 128 + lane;
+        // Every slab load is unconditional (indices past the last slab
+        // re-read it), so none waits in a branch; the sum takes the splits.
+#pragma unroll
+        for (uint32_t sp = 0; sp < kBlockQknMaxSplits; ++sp) {
+          const uint64_t off = (uint64_t)min(sp, qk.splits - 1) * slab;
+          pa[u][sp] = pp[off];
+          pb[u][sp] = pp[off + 64];
+        }
+      }
+      uint32_t page[2], wa[2], wb[2];
+      float c[2], sn[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        page[u] = table[(uint64_t)rows_u[u] * stride + min(pos[u] / 16, stride - 1)];
+        const uint16_t* wn = roles[u] < (uint32_t)G ? qk.q_norm : qk.k_norm;
+        wa[u] = wn[lane];
+        wb[u] = wn[lane + 64];
+        const uint32_t trig = (pos[u] < context ? pos[u] : 0) * 64 + lane;
+        c[u] = qk.cos_t[trig];
+        sn[u] = qk.sin_t[trig];
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (hr0 + u * kWaves >= nwork) break;
+        const uint32_t role = roles[u], i = rows_u[u] - row0, pu = pos[u];
+        const bool slot_ok = pu < context && pu / 16 < stride && page[u] < pages;
+        // h = (P_0 + P_1 + ...) in split order, rounded once (the QK-norm kernel's order).
+        float a = pa[u][0], bsum = pb[u][0];
+#pragma unroll
+        for (uint32_t sp = 1; sp < kBlockQknMaxSplits; ++sp) {
+          if (sp < qk.splits) {
+            a += pa[u][sp];
+            bsum += pb[u][sp];
+          }
+        }
+        a = round_bf16(a);
+        bsum = round_bf16(bsum);
+        if (!slot_ok && h == 0 && role == 0 && lane == 0) raise_error(err, ERR_PAGE);
+        uint32_t ra, rb;
+        if (role == (uint32_t)G + 1) {
+          ra = f32_to_bf16(a);  // the value head: raw
+          rb = f32_to_bf16(bsum);
+        } else {
+          bad |= qknorm_rope_wave_head(a, bsum, bf16_to_f32(wa[u]), bf16_to_f32(wb[u]), c[u], sn[u], qk.eps, ra, rb);
+        }
+        uint16_t* ls =
+            role < (uint32_t)G ? qkn_q + (i * G + role) * 128 : (role == (uint32_t)G ? qkn_k : qkn_v) + i * 128;
+        ls[lane] = (uint16_t)ra;
+        ls[lane + 64] = (uint16_t)rb;
+        if (role >= (uint32_t)G && slot_ok) {
+          uint16_t* dst = (role == (uint32_t)G ? qk.k_cache : qk.v_cache) +
+                          (((uint64_t)page[u] * 16 + (pu & 15u)) * kvh + h) * 128;
+          dst[lane] = (uint16_t)ra;
+          dst[lane + 64] = (uint16_t)rb;
+        }
+      }
+    }
+    __syncthreads();
+    if (qvalid) {
+      const uint16_t* qp = qkn_q + (rj * G + j % G) * 128 + 8 * g16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
   const float scale = __builtin_bit_cast(float, kScaleBitsB);
   const float kNegInf = -__builtin_inff();
   float m_run = kNegInf, l_run = 0.f;
@@ -169,6 +283,18 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
     const bool here = !LAST || PH == 1 || p < npages;  // the phase has a page this iteration
     const int b = it & 1;
     if (here) {
+      if constexpr (QKN) {
+        // The block's own new slots (positions pos0 .. pmax) come from LDS.
+        if (p * 16 + 15 >= pos0) {
+          const uint32_t tk = p * 16 + lt;
+          if (tk >= pos0 && tk <= pmax) kreg = *reinterpret_cast<const u32x4*>(qkn_k + (tk - pos0) * 128 + 8 * lc);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t tv = p * 16 + 4 * wave + t;
+            if (tv >= pos0 && tv <= pmax) vreg[t] = reinterpret_cast<const uint32_t*>(qkn_v + (tv - pos0) * 128)[lane];
+          }
+        }
+      }
       ktile[b][lt][lc] = kreg;
       if (LAST && p + 1 == npages) {
 #pragma unroll
@@ -326,34 +452,48 @@ hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, c
                                    const uint32_t* positions, const uint32_t* table, const uint32_t* blocks,
                                    uint32_t nblocks, uint16_t* out, uint32_t out_tiled, uint32_t out_rows,
                                    uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                                   uint32_t* err, hipStream_t s) {
+                                   uint32_t* err, hipStream_t s, const AttnQkn* qkn) {
   if (nblocks == 0) return hipSuccess;
+  if (qkn && !attention_blocks_qkn_supported(qh, kvh, qkn->splits)) return hipErrorInvalidValue;
   const uint32_t mt = out_tiled ? act_mtiles(out_rows) : 0u;
   const dim3 grid(nblocks, kvh);
+  const AttnQkn qa = qkn ? *qkn : AttnQkn{};
   // Page phases so that a small grid still puts about four waves on each
   // SIMD (256 CUs): a workgroup of 4 PH waves per block and head.
   const uint64_t wgs = (uint64_t)nblocks * kvh;
   const int ph = wgs <= 256 ? 4 : wgs <= 512 ? 2 : 1;
-#define FH_BLOCKS_PH(G_, PH_)                                                                                      \
-  hipLaunchKernelGGL((attn_block_kernel<G_, PH_>), grid, dim3(256 * PH_), 0, s, q, k_cache, v_cache, positions, \
-                     table, blocks, out, mt, qh, kvh, stride, pages, context, err)
-#define FH_BLOCKS(G_)                  \
-  if (ph == 4)                         \
-    FH_BLOCKS_PH(G_, 4);               \
-  else if (ph == 2)                    \
-    FH_BLOCKS_PH(G_, 2);               \
-  else                                 \
-    FH_BLOCKS_PH(G_, 1)
+#define FH_BLOCKS_PH(G_, PH_, QKN_)                                                                               \
+  hipLaunchKernelGGL((attn_block_kernel<G_, PH_, QKN_>), grid, dim3(256 * PH_), 0, s, q, k_cache, v_cache,        \
+                     positions, table, blocks, out, mt, qh, kvh, stride, pages, context, err, qa)
+#define FH_BLOCKS_Q(G_, QKN_)      \
+  if (ph == 4)                     \
+    FH_BLOCKS_PH(G_, 4, QKN_);     \
+  else if (ph == 2)                \
+    FH_BLOCKS_PH(G_, 2, QKN_);     \
+  else                             \
+    FH_BLOCKS_PH(G_, 1, QKN_)
+#define FH_BLOCKS(G_)        \
+  if (qkn) {                 \
+    FH_BLOCKS_Q(G_, true);   \
+  } else {                   \
+    FH_BLOCKS_Q(G_, false);  \
+  }
   switch (qh / kvh) {
     case 1: FH_BLOCKS(1); break;
     case 2: FH_BLOCKS(2); break;
     case 4: FH_BLOCKS(4); break;
-    case 8: FH_BLOCKS(8); break;
+    case 8: FH_BLOCKS_Q(8, false); break;
     default: return hipErrorInvalidValue;
   }
 #undef FH_BLOCKS
+#undef FH_BLOCKS_Q
 #undef FH_BLOCKS_PH
   return hipGetLastError();
+}
+
+bool attention_blocks_qkn_supported(uint32_t qh, uint32_t kvh, uint32_t qkv_splits) {
+  return kvh && qh % kvh == 0 && qh / kvh <= 4 && (qh / kvh & (qh / kvh - 1)) == 0 && qkv_splits >= 1 &&
+         qkv_splits <= kBlockQknMaxSplits;
 }
 
 }  // namespace fh

@@ -210,12 +210,17 @@ hipError_t launch_attention_merge(const float* partials, const uint32_t* positio
 // k_attention_block.hip). blocks[i] = first row | (rows << 16); each block
 // has at most attention_block_rows(qh, kvh) rows at consecutive positions,
 // and its last row's page table serves all of them. No scratch, no merge.
+// qkn != nullptr: the QK-norm, RoPE and KV append of every block row run in
+// the attention workgroups (AttnQkn as for the decode partitions; q unused).
+// The caller guarantees that no block's pages hold a slot another block of
+// the launch writes.
 uint32_t attention_block_rows(uint32_t qh, uint32_t kvh);
+bool attention_blocks_qkn_supported(uint32_t qh, uint32_t kvh, uint32_t qkv_splits);
 hipError_t launch_attention_blocks(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                    const uint32_t* positions, const uint32_t* table, const uint32_t* blocks,
                                    uint32_t nblocks, uint16_t* out, uint32_t out_tiled, uint32_t out_rows,
                                    uint32_t qh, uint32_t kvh, uint32_t stride, uint32_t pages, uint32_t context,
-                                   uint32_t* err, hipStream_t s);
+                                   uint32_t* err, hipStream_t s, const AttnQkn* qkn = nullptr);
 
 // logits
 // With host_choices (coherent pinned memory), the choices and the error word

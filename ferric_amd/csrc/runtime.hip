@@ -20,6 +20,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/ferric_hip.h"
@@ -975,11 +976,60 @@ fh_status fh_write_kv_page(fh_ctx* ctx, uint32_t layer, uint32_t which, uint32_t
   return FH_OK;
 }
 
+// Attention blocks of a prefill chunk: runs of rows of one sequence at
+// consecutive positions whose page lists extend one another (so the block's
+// last row's table serves every row of it), at most attention_block_rows()
+// rows each, stored as first row | rows << 16. Longest first: a block reads
+// the pages up to its last row's position, and workgroups are dispatched in
+// block order, so the short ones fill the tail.
+uint32_t prefill_blocks(const fh_ctx* ctx, const fh_row* rows, uint32_t nrows, uint32_t* blocks) {
+  const uint32_t bq = fh::attention_block_rows(ctx->md.query_heads, ctx->md.kv_heads);
+  uint32_t nblocks = 0;
+  for (uint32_t i = 0; i < nrows;) {
+    uint32_t j = i + 1;
+    while (j < nrows && j - i < bq && rows[j].sequence == rows[i].sequence &&
+           rows[j].position == rows[j - 1].position + 1 && rows[j].page_count >= rows[j - 1].page_count &&
+           std::memcmp(rows[j].pages, rows[j - 1].pages, (size_t)rows[j - 1].page_count * 4) == 0)
+      ++j;
+    blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
+    i = j;
+  }
+  std::stable_sort(blocks, blocks + nblocks, [&](uint32_t a, uint32_t b) {
+    return rows[(a & 0xffffu) + (a >> 16) - 1].position > rows[(b & 0xffffu) + (b >> 16) - 1].position;
+  });
+  return nblocks;
+}
+
+// Whether no block reads a slot that another block writes: the pages holding
+// a block's positions are listed, up to its last position, by no other
+// block's last row (the table that block's attention reads). Then each block
+// can append its own rows' K/V inside its attention workgroups.
+bool prefill_blocks_private(const fh_row* rows, const uint32_t* blocks, uint32_t nblocks) {
+  std::unordered_map<uint32_t, uint32_t> writer;  // physical page -> writing block
+  for (uint32_t b = 0; b < nblocks; ++b) {
+    const uint32_t i = blocks[b] & 0xffffu, n = blocks[b] >> 16;
+    const fh_row& last = rows[i + n - 1];
+    for (uint32_t pi = rows[i].position / 16; pi <= last.position / 16; ++pi) {
+      const auto ins = writer.emplace(last.pages[pi], b);
+      if (!ins.second && ins.first->second != b) return false;
+    }
+  }
+  for (uint32_t b = 0; b < nblocks; ++b) {
+    const uint32_t i = blocks[b] & 0xffffu, n = blocks[b] >> 16;
+    const fh_row& last = rows[i + n - 1];
+    for (uint32_t pi = 0; pi <= last.position / 16; ++pi) {
+      const auto it = writer.find(last.pages[pi]);
+      if (it != writer.end() && it->second != b) return false;
+    }
+  }
+  return true;
+}
+
 // Enqueues (or, dry, only counts) the launches of a prefill chunk of R rows
 // with nout output rows, whose metadata (tokens, positions, output rows,
 // nblocks attention blocks, page tables) is already in pre.d_meta.
-hipError_t enqueue_prefill(fh_ctx* ctx, uint32_t R, uint32_t nout, uint32_t nblocks, uint64_t* launches,
-                           bool dry = false) {
+hipError_t enqueue_prefill(fh_ctx* ctx, uint32_t R, uint32_t nout, uint32_t nblocks, bool blocks_private,
+                           uint64_t* launches, bool dry = false) {
   const fh_model_desc& md = ctx->md;
   const fh_ctx_options& op = ctx->opt;
   auto& p = ctx->pre;
@@ -1010,6 +1060,11 @@ hipError_t enqueue_prefill(fh_ctx* ctx, uint32_t R, uint32_t nout, uint32_t nblo
   const bool split_k = R <= fh::kPanelRows;
   const uint32_t sq = R <= kMaxRows ? ctx->s_qkv : p.s_qkv, so = R <= kMaxRows ? ctx->s_o : p.s_o,
                  sd = R <= kMaxRows ? ctx->s_down : p.s_down;
+  // Split-K chunks whose blocks write no slot another block reads run the
+  // QK-norm, RoPE and KV append inside the attention workgroups (one launch
+  // fewer per layer).
+  const bool qkn_blocks = split_k && !fused_qkv && blocks_private &&
+                          fh::attention_blocks_qkn_supported(QH, KVH, sq);
   L(FH_KC_EMBEDDING, [&] { return fh::launch_clear_word(err, s); });
   L(FH_KC_EMBEDDING, [&] { return fh::launch_embedding(d_tok, ctx->embed, p.hidden, R, H, V, err, s); });
   for (uint32_t l = 0; l < md.layers; ++l) {
@@ -1032,15 +1087,18 @@ hipError_t enqueue_prefill(fh_ctx* ctx, uint32_t R, uint32_t nout, uint32_t nblo
                        : fh::launch_gemm_large(p.xn, W.qkv, R, ctx->nqkv, H, FH_EPI_BF16, nullptr, p.qkv,
                                                ctx->nqkv, err, s);
       });
-      L(FH_KC_QKNORM_ROPE_KV, [&] {
-        return fh::launch_qknorm_rope_kv(split_k ? nullptr : p.qkv, split_k ? p.part : nullptr, split_k ? sq : 0,
-                                         W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, p.qrot, kc, vc,
-                                         R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
-      });
+      if (!qkn_blocks)
+        L(FH_KC_QKNORM_ROPE_KV, [&] {
+          return fh::launch_qknorm_rope_kv(split_k ? nullptr : p.qkv, split_k ? p.part : nullptr, split_k ? sq : 0,
+                                           W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t, d_pos, d_tab, p.qrot, kc, vc,
+                                           R, QH, KVH, stride, pages, C, md.rms_epsilon, err, s);
+        });
     }
+    const fh::AttnQkn qa{p.part, sq, fh::partial_slab_rows(R), W.q_norm, W.k_norm, ctx->cos_t, ctx->sin_t,
+                         kc,     vc, md.rms_epsilon};
     L(FH_KC_ATTENTION, [&] {
       return fh::launch_attention_blocks(p.qrot, kc, vc, d_pos, d_tab, d_blocks, nblocks, p.attn, 1, R, QH, KVH,
-                                         stride, pages, C, err, s);
+                                         stride, pages, C, err, s, qkn_blocks ? &qa : nullptr);
     });
     if (split_k) {
       L(FH_KC_O_GEMM, [&] {
@@ -1130,25 +1188,8 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
     std::fill(t + rows[i].page_count, t + stride, 0xffffffffu);
   }
   for (uint32_t i = 0; i < nout; ++i) outs[i] = output_rows[i];
-  // Attention blocks: runs of rows of one sequence at consecutive positions
-  // whose page lists extend one another (so the block's last row's table
-  // serves every row of it), at most attention_block_rows() rows each.
-  const uint32_t bq = fh::attention_block_rows(QH, KVH);
-  uint32_t nblocks = 0;
-  for (uint32_t i = 0; i < nrows;) {
-    uint32_t j = i + 1;
-    while (j < nrows && j - i < bq && rows[j].sequence == rows[i].sequence &&
-           rows[j].position == rows[j - 1].position + 1 && rows[j].page_count >= rows[j - 1].page_count &&
-           std::memcmp(rows[j].pages, rows[j - 1].pages, (size_t)rows[j - 1].page_count * 4) == 0)
-      ++j;
-    blocks[nblocks++] = i | ((j - i) << 16);  // i < 16384, j - i <= 64
-    i = j;
-  }
-  // Longest first: a block reads the pages up to its last row's position, and
-  // workgroups are dispatched in block order, so the short ones fill the tail.
-  std::stable_sort(blocks, blocks + nblocks, [&](uint32_t a, uint32_t b) {
-    return rows[(a & 0xffffu) + (a >> 16) - 1].position > rows[(b & 0xffffu) + (b >> 16) - 1].position;
-  });
+  const uint32_t nblocks = prefill_blocks(ctx, rows, nrows, blocks);
+  const bool priv = nrows <= fh::kPanelRows && prefill_blocks_private(rows, blocks, nblocks);
   auto poison = [&](fh_status s2, const std::string& msg) {
     ctx->poisoned = true;
     return fail(ctx, s2, msg);
@@ -1161,7 +1202,7 @@ fh_status run_prefill(fh_ctx* ctx, uint64_t batch_id, const fh_row* rows, uint32
   hipEventRecord(ctx->ev_begin, s);
   if (ctx->profiling) ctx->prof_launches.clear();
   uint64_t n = 0;
-  e = enqueue_prefill(ctx, nrows, nout, nblocks, &n);
+  e = enqueue_prefill(ctx, nrows, nout, nblocks, priv, &n);
   if (e != hipSuccess) return poison(FH_ERR_DEVICE, std::string("launch: ") + hipGetErrorString(e) + ctx->launch_detail);
   hipEventRecord(ctx->ev_end, s);
   if (nout) e = hipMemcpyAsync(p.h_out, p.choices, nout * 4, hipMemcpyDeviceToHost, s);
@@ -1310,8 +1351,12 @@ fh_status fh_expected_dispatch_count(fh_ctx* ctx, uint64_t batch_id, const fh_ro
   fh_status st = validate_batch(ctx, batch_id, rows, nrows, output_rows, nout);
   if (st != FH_OK) return st;
   uint64_t n = 0;
-  if (nrows > ctx->opt.row_capacity)
-    enqueue_prefill(ctx, nrows, nout, 0, &n, true);
+  if (nrows > ctx->opt.row_capacity) {
+    std::vector<uint32_t> blocks(nrows);
+    const uint32_t nblocks = prefill_blocks(ctx, rows, nrows, blocks.data());
+    const bool priv = nrows <= fh::kPanelRows && prefill_blocks_private(rows, blocks.data(), nblocks);
+    enqueue_prefill(ctx, nrows, nout, nblocks, priv, &n, true);
+  }
   else
     enqueue_step(ctx, nrows, &n, true);
   *count = n;

@@ -36,16 +36,18 @@ def decode_launches(layers, qk_in_attention, merge_in_attention, capture=False, 
     return 5 + layers * per_layer + (layers if capture else 0) - norms
 
 
-def prefill_launches(layers, rows, outputs):
+def prefill_launches(layers, rows, outputs, private=True):
     """Launches of a prefill chunk: clear, embedding; per layer the chunk's
     schedule (over 256 rows: norm, QKV with the QK-norm in its epilogue,
     attention, O + residual, norm, gate/up, down + residual; up to 256 rows:
-    split-K partials folded by the norms, the input norm launched once);
-    then gather, final norm, head and two argmax passes for the output rows."""
+    split-K partials folded by the norms, the input norm launched once, and,
+    where no attention block reads a slot another block writes (`private`),
+    the QK-norm inside the attention launch); then gather, final norm, head
+    and two argmax passes for the output rows."""
     head = 5 if outputs else 0
     if rows > 256:
         return 2 + 7 * layers + head
-    return 2 + 1 + 8 * layers + head
+    return 2 + 1 + (7 if private else 8) * layers + head
 
 
 def run_checked(runner, pool, rows, outs=None, expect=None):
@@ -121,6 +123,11 @@ def test_8b_prefill_chunks(runner8b):
     sids = [pool.admit(0) for _ in range(3)]
     rows = [(s, 5 + t) for s in sids for t in range(14)]
     run_checked(runner, pool, rows, outs=[], expect=prefill_launches(L8, 42, 0))
+    # 42 rows of one sequence: three attention blocks, the later ones reading
+    # the pages the earlier ones write, so the QK-norm keeps its own launch.
+    seq = pool.admit(0)
+    rows = [(seq, 3 + t) for t in range(42)]
+    run_checked(runner, pool, rows, outs=[41], expect=prefill_launches(L8, 42, 1, private=False))
 
 
 def test_0_6b_batch32_and_capture():

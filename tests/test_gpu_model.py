@@ -643,6 +643,57 @@ def test_prefill_chunk_8b_fused_qkv_epilogue():
     _prefill_case(cfg, limits, [150, 140], [100, 3000], 512, 43, "prefill 8b fused qkv")
 
 
+def test_prefill_qknorm_inside_block_attention_is_bit_identical():
+    # A chunk of up to 256 rows whose attention blocks write no slot another
+    # block reads runs the QK-norm, RoPE and KV append inside the attention
+    # workgroups. Three 14-token prompts alone take that form; the same three
+    # prompts next to a 20-token prompt of a fourth sequence (two blocks, the
+    # second reading the first's page) keep the separate QK-norm launch. A
+    # row's projections do not depend on the other rows of a 33-256-row
+    # chunk, so the three sequences' K/V slots and output logits must be equal
+    # bit for bit between the two runs.
+    cfg = dict(ferric_amd.QWEN3_8B, layers=2)
+    limits = PagedLimits(context_tokens=256, physical_page_count=64, page_table_stride=16)
+    rng = np.random.default_rng(71)
+    prompts = [rng.integers(0, cfg["vocabulary"], 14) for _ in range(3)]
+    extra = rng.integers(0, cfg["vocabulary"], 20)
+    got = []
+    for with_extra in (False, True):
+        runner = TpBatchRunner(cfg, limits, row_capacity=32, use_graphs=False, prefill_rows=256)
+        try:
+            runner.synthesize_weights(71, 0.02)
+            pool = PagePool(limits, seed=72)
+            sids = [pool.admit(0) for _ in range(3)]
+            rows = [(s, int(t)) for s, p in zip(sids, prompts) for t in p]
+            outs = [13, 27, 41]
+            if with_extra:
+                e = pool.admit(0)
+                rows += [(e, int(t)) for t in extra]
+            batch = pool.prepare(rows)
+            (pre,) = runner.expected_dispatch_counts_for_selection(batch, outs)
+            (before,) = runner.dispatch_counts()
+            choices = runner.execute_batch(batch, outs).choices
+            (after,) = runner.dispatch_counts()
+            assert after - before == pre
+            logits = runner.read_logits()[: len(outs)].copy()
+            # keyed by (layer, K or V, sequence, logical page): the two pools
+            # need not place the sequences on the same physical pages
+            kv = {(layer, which, i, lp): runner.read_kv_page(layer, which, int(pg))
+                  for layer in range(cfg["layers"]) for which in (0, 1)
+                  for i, s in enumerate(sids) for lp, pg in enumerate(pool.sequences[s].pages)}
+            got.append((pre, choices, logits, kv))
+        finally:
+            runner.close()
+    (pre_a, ch_a, lg_a, kv_a), (pre_b, ch_b, lg_b, kv_b) = got
+    # One launch per layer fewer in the fused form.
+    assert pre_b - pre_a == cfg["layers"], (pre_a, pre_b)
+    assert list(ch_a) == list(ch_b)
+    assert np.array_equal(lg_a.view(np.uint32), lg_b.view(np.uint32)), "output logits"
+    assert kv_a.keys() == kv_b.keys()
+    for key in kv_a:
+        assert np.array_equal(kv_a[key], kv_b[key]), key
+
+
 def test_prefill_continuation_and_interleaved_rows():
     # 0.6B shape, 2 layers. Prefill attention groups runs of rows of one
     # sequence at consecutive positions into blocks: a 70-row continuation of
