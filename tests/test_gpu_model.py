@@ -550,6 +550,40 @@ def test_device_error_of_a_decode_step_reaches_the_host(graphs):
         r.close()
 
 
+@pytest.mark.parametrize("private", [True, False])
+def test_device_error_of_a_prefill_chunk_reaches_the_host(private):
+    # A 42-row prefill chunk (the split-K panel path) with a NaN planted in
+    # layer 0's query norm weight: the QK-norm's nonfinite check must fail the
+    # chunk with FH_ERR_NONFINITE, whether the QK-norm runs inside the block
+    # attention (three prompts, one block each) or in its own launch (one
+    # prompt in three blocks, the later ones reading the earlier ones' pages).
+    from ferric_amd import _lib
+
+    cfg = dict(ferric_amd.QWEN3_8B, layers=1)
+    limits = PagedLimits(context_tokens=256, physical_page_count=32, page_table_stride=16)
+    r = TpBatchRunner(cfg, limits, row_capacity=8, use_graphs=False, prefill_rows=64)
+    try:
+        r.synthesize_weights(9, 0.02)
+        qn = r.download_weight(_lib.QUERY_NORM, 0, 128)
+        qn[5] = 0x7FC0
+        r.upload_weight(_lib.QUERY_NORM, 0, qn)
+        pool = PagePool(limits, seed=9)
+        if private:
+            sids = [pool.admit(0) for _ in range(3)]
+            rows = [(s, 7 + t) for s in sids for t in range(14)]
+        else:
+            s = pool.admit(0)
+            rows = [(s, 7 + t) for t in range(42)]
+        batch = pool.prepare(rows)
+        (pre,) = r.expected_dispatch_counts_for_selection(batch, [41])
+        assert pre == 2 + 1 + (7 if private else 8) * cfg["layers"] + 5, pre
+        with pytest.raises(FerricError) as e:
+            r.execute_batch(batch, [41])
+        assert e.value.status == 6, e.value
+    finally:
+        r.close()
+
+
 def test_full_small_model_prompt_then_greedy_decode():
     # Qwen3-0.6B shape, all 28 layers, batch 1: a 16-token prompt as one
     # 16-row batch, then 8 greedy decode steps (teacher-forced).
