@@ -164,6 +164,9 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t qkn_q[QKN ? kBlockRows * G * 128 : 1];
   __shared__ __attribute__((aligned(16))) uint16_t qkn_k[QKN ? kBlockRows * 128 : 1];
   __shared__ __attribute__((aligned(16))) uint16_t qkn_v[QKN ? kBlockRows * 128 : 1];
+  // A round's squares (head-row slot, element) and their serial sums.
+  __shared__ float qkn_sq[QKN ? 2 * 4 * PH : 1][QKN ? 129 : 1];
+  __shared__ float qkn_sum[QKN ? 2 * 4 * PH : 1];
   uint32_t pos0 = 0;
   if constexpr (QKN) {
     pos0 = positions[row0];
@@ -175,7 +178,9 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
     // role): roles 0..G-1 the query heads h G + role, G the key head and
     // G + 1 the value head of KV head h.
     constexpr uint32_t kWaves = 4 * PH;
-    for (uint32_t hr0 = w; hr0 < nwork; hr0 += 2 * kWaves) {
+    const uint32_t rounds = (nwork + 2 * kWaves - 1) / (2 * kWaves);  // uniform: the loop holds barriers
+    for (uint32_t rd = 0; rd < rounds; ++rd) {
+      const uint32_t hr0 = rd * 2 * kWaves + w;
       uint32_t hrs[2], rows_u[2], roles[2], pos[2];
       float pa[2][kBlockQknMaxSplits], pb[2][kBlockQknMaxSplits];
 #pragma unroll
@@ -212,12 +217,13 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
         c[u] = qk.cos_t[trig];
         sn[u] = qk.sin_t[trig];
       }
+      // h = (P_0 + P_1 + ...) in split order, rounded once (the QK-norm
+      // kernel's order). The squares go to LDS, and one lane per head-row
+      // adds its 128 squares in element order (the wave routine's serial
+      // sum, with no chain of lane reads), then the wave finishes the head.
+      float fa[2], fb[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        if (hr0 + u * kWaves >= nwork) break;
-        const uint32_t role = roles[u], i = rows_u[u] - row0, pu = pos[u];
-        const bool slot_ok = pu < context && pu / 16 < stride && page[u] < pages;
-        // h = (P_0 + P_1 + ...) in split order, rounded once (the QK-norm kernel's order).
         float a = pa[u][0], bsum = pb[u][0];
 #pragma unroll
         for (uint32_t sp = 1; sp < kBlockQknMaxSplits; ++sp) {
@@ -226,15 +232,33 @@ __global__ __launch_bounds__(256 * PH, 4) void attn_block_kernel(
             bsum += pb[u][sp];
           }
         }
-        a = round_bf16(a);
-        bsum = round_bf16(bsum);
+        fa[u] = round_bf16(a);
+        fb[u] = round_bf16(bsum);
+        const int slot = w + u * kWaves;
+        qkn_sq[slot][lane] = fa[u] * fa[u];
+        qkn_sq[slot][64 + lane] = fb[u] * fb[u];
+      }
+      __syncthreads();
+      if (threadIdx.x < 2 * kWaves) {
+        float sum = 0.f;
+#pragma unroll 16
+        for (int l = 0; l < 128; ++l) sum = sum + qkn_sq[threadIdx.x][l];
+        qkn_sum[threadIdx.x] = sum;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (hr0 + u * kWaves >= nwork) break;
+        const uint32_t role = roles[u], i = rows_u[u] - row0, pu = pos[u];
+        const bool slot_ok = pu < context && pu / 16 < stride && page[u] < pages;
         if (!slot_ok && h == 0 && role == 0 && lane == 0) raise_error(err, ERR_PAGE);
         uint32_t ra, rb;
         if (role == (uint32_t)G + 1) {
-          ra = f32_to_bf16(a);  // the value head: raw
-          rb = f32_to_bf16(bsum);
+          ra = f32_to_bf16(fa[u]);  // the value head: raw
+          rb = f32_to_bf16(fb[u]);
         } else {
-          bad |= qknorm_rope_wave_head(a, bsum, bf16_to_f32(wa[u]), bf16_to_f32(wb[u]), c[u], sn[u], qk.eps, ra, rb);
+          bad |= qknorm_rope_wave_head_from_sum(fa[u], fb[u], qkn_sum[w + u * kWaves], bf16_to_f32(wa[u]),
+                                                bf16_to_f32(wb[u]), c[u], sn[u], qk.eps, ra, rb);
         }
         uint16_t* ls =
             role < (uint32_t)G ? qkn_q + (i * G + role) * 128 : (role == (uint32_t)G ? qkn_k : qkn_v) + i * 128;

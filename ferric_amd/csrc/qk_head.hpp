@@ -74,15 +74,12 @@ __device__ __forceinline__ uint32_t norm_weight_bf16_int(float x, float inv, flo
 // when a value or the sum is nonfinite. The decode QK-norm kernel and the
 // decode attention kernel's fused form both call this, so their outputs are
 // bit-identical.
-__device__ __forceinline__ bool qknorm_rope_wave_head(float a, float b, float wa, float wb, float c, float s,
-                                                      float eps, uint32_t& ra, uint32_t& rb) {
+// The part after the square sum, given it (the block attention forms the
+// sums of its heads another way, in the same order).
+__device__ __forceinline__ bool qknorm_rope_wave_head_from_sum(float a, float b, float sum, float wa, float wb,
+                                                               float c, float s, float eps, uint32_t& ra,
+                                                               uint32_t& rb) {
   bool bad = !is_finite_f32(a) | !is_finite_f32(b);
-  const float sqa = a * a, sqb = b * b;
-  float sum = 0.f;
-#pragma unroll
-  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqa, l);
-#pragma unroll
-  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqb, l);
   const float inv = inverse_rms(sum, 128.0f, eps);
   bad |= !is_finite_f32(sum) | !is_finite_f32(inv);
   const float an = bf16_to_f32(norm_weight_bf16(a, inv, wa));
@@ -92,6 +89,17 @@ __device__ __forceinline__ bool qknorm_rope_wave_head(float a, float b, float wa
   rb = f32_to_bf16(b_cos + a_sin);
   bad |= ((ra & 0x7f80u) == 0x7f80u) | ((rb & 0x7f80u) == 0x7f80u);
   return bad;
+}
+
+__device__ __forceinline__ bool qknorm_rope_wave_head(float a, float b, float wa, float wb, float c, float s,
+                                                      float eps, uint32_t& ra, uint32_t& rb) {
+  const float sqa = a * a, sqb = b * b;
+  float sum = 0.f;
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqa, l);
+#pragma unroll
+  for (int l = 0; l < 64; ++l) sum = sum + lane_bcast(sqb, l);
+  return qknorm_rope_wave_head_from_sum(a, b, sum, wa, wb, c, s, eps, ra, rb);
 }
 
 struct QkvRopeArgs {
