@@ -350,6 +350,31 @@ def test_small_batches_merge_attention_partitions_in_kernel():
             pair.close()
 
 
+def test_short_context_capacity_takes_one_partition():
+    # A context capacity of 257..512 tokens takes one 32-page partition per
+    # row whatever the batch (no partition records, no merge; the speculative
+    # draft's form). Against the oracle, two steps each through the graph
+    # path: the 0.6B shape at 7 rows (16-page partitions otherwise) with the
+    # QK-norm inside the partitions, and the 8B shape at 2 rows (2 x 32 query
+    # heads, also 16-page otherwise).
+    cases = [(dict(ferric_amd.QWEN3_0_6B, layers=2), [0, 15, 100, 257, 300, 480, 500]),
+             (dict(ferric_amd.QWEN3_8B, layers=2), [301, 497])]
+    limits = PagedLimits(context_tokens=512, physical_page_count=256, page_table_stride=32)
+    for cfg, lengths in cases:
+        pair = Pair(cfg, limits, seed=29, rows=len(lengths), graphs=True)
+        try:
+            sids = pair.admit_with_prefix(lengths)
+            toks = [int(t) for t in np.random.default_rng(len(lengths)).integers(0, cfg["vocabulary"], len(sids))]
+            for step in range(2):
+                batch, out, ref = pair.step(list(zip(sids, toks)))
+                _mark_written(pair, batch)
+                pair.check(batch, out, ref, f"{cfg['hidden']} x {len(lengths)} rows at capacity 512, step {step}")
+                toks = [int(c) for c in ref["choices"]]
+            pair.check_kv()
+        finally:
+            pair.close()
+
+
 GOLDEN_SPREAD = Path(__file__).resolve().parent / "golden" / "reduction_spread.json"
 
 
