@@ -75,6 +75,8 @@ def parse():
                    + sorted(SPEC_WORKLOADS))
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-spec-prompt", type=int, default=16, help="speculative CPU baseline: prompt tokens")
+    p.add_argument("--cpu-spec-rounds", type=int, default=12, help="speculative CPU baseline: rounds")
     p.add_argument("--cpu-steps", type=int, default=2, help="decode steps the CPU oracle sample runs")
     p.add_argument("--cpu-prefill-tokens", type=int, default=256,
                    help="prompt tokens of the one sequence the prefill workload's CPU oracle sample prefills")
@@ -464,7 +466,68 @@ def speculative_bench(args, name):
     }
     target.close()
     draft.close()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = speculative_cpu_baseline(ferric_amd.QWEN3_8B, ferric_amd.QWEN3_0_6B, k,
+                                                          args.cpu_spec_prompt, args.cpu_spec_rounds, args.seed)
     print(json.dumps(result), flush=True)
+
+
+def speculative_cpu_baseline(cfg_t, cfg_d, k, prompt_len, rounds, seed):
+    """The CPU oracle running greedy speculation for one sequence: the
+    prompt through both models, then `rounds` rounds of k draft decode steps
+    (one row each) and a (k + 1)-row target verify, the accepted prefix and
+    the target's next token emitted, positions advanced by what was emitted
+    (a full accept adds the draft's catch-up step)."""
+    from oracle import oracle as orc
+
+    ctx = (prompt_len + (rounds + 1) * (k + 1) + 15) // 16 * 16
+    stride = ctx // 16
+    mt, md = orc.Model(cfg_t, stride), orc.Model(cfg_d, stride)
+    try:
+        t0 = time.perf_counter()
+        mt.synthesize(seed, 0.02)
+        md.synthesize(seed + 1, 0.02)
+        setup_s = time.perf_counter() - t0
+        rows = max(prompt_len, k + 1)
+        table = np.tile(np.arange(stride, dtype=np.uint32), (rows, 1))
+        counts = np.full(rows, stride, np.uint32)
+        prompt = [int(t) for t in np.random.default_rng(seed).integers(0, cfg_t["vocabulary"], prompt_len)]
+        t1 = time.perf_counter()
+        n = prompt_len
+        anchor = int(mt.forward(prompt, np.arange(n), table[:n], counts[:n], stride, want_logits=False)["choices"][-1])
+        md.forward(prompt, np.arange(n), table[:n], counts[:n], stride, want_logits=False)
+        pos, emitted, accepted = n, 0, 0
+        for _ in range(rounds):
+            drafts, tok = [], anchor
+            for i in range(k):
+                tok = int(md.forward([tok], [pos + i], table[:1], counts[:1], stride, want_logits=False)["choices"][0])
+                drafts.append(tok)
+            ids = [anchor] + drafts
+            c = [int(x) for x in mt.forward(ids, np.arange(pos, pos + k + 1), table[:k + 1], counts[:k + 1], stride,
+                                            want_logits=False)["choices"]]
+            acc = 0
+            while acc < k and drafts[acc] == c[acc]:
+                acc += 1
+            if acc == k:  # the draft never saw its last token
+                md.forward([drafts[-1]], [pos + k], table[:1], counts[:1], stride, want_logits=False)
+            emitted += acc + 1
+            accepted += acc
+            anchor = c[acc]
+            pos += acc + 1
+        elapsed = time.perf_counter() - t1
+        return {
+            "value": round(emitted / elapsed, 2),
+            "unit": "tokens/s",
+            "cores": orc.threads(),
+            "kind": "port",
+            "sample": (f"one sequence: a {prompt_len}-token prompt through both models, then {rounds} rounds of "
+                       f"{k} draft steps ({cfg_d['layers']} layers) and a {k + 1}-row verify ({cfg_t['layers']} "
+                       f"layers), {emitted} tokens emitted ({accepted} drafts accepted) in {elapsed:.2f} s, tokens/s "
+                       f"of that sample (the GPU leg runs 32 sequences); weight generation {setup_s:.1f} s untimed"),
+        }
+    finally:
+        mt.close()
+        md.close()
 
 
 TRAFFIC_PROFILE = "profiles/attention_decode_qwen3_8b_b32_hbm_counters.md"
