@@ -753,24 +753,25 @@ def test_prefill_qknorm_inside_block_attention_is_bit_identical():
         assert np.array_equal(kv_a[key], kv_b[key]), key
 
 
-def test_prefill_chunk_of_single_row_blocks_with_the_qknorm_inside():
-    # 80 sequences with prefixes of 0..600 tokens, one new row each, as one
-    # prefill chunk: 80 one-row attention blocks x 8 KV heads (640
-    # workgroups: one page phase), none reading another's written slot, so
-    # the QK-norm, RoPE and KV append run inside the block attention. Against
-    # the oracle, then the written slots.
+@pytest.mark.parametrize("nseq", [40, 80])
+def test_prefill_chunk_of_single_row_blocks_with_the_qknorm_inside(nseq):
+    # nseq sequences with prefixes of 0..600 tokens, one new row each, as one
+    # prefill chunk: nseq one-row attention blocks x 8 KV heads (320
+    # workgroups: two page phases; 640: one), none reading another's written
+    # slot, so the QK-norm, RoPE and KV append run inside the block
+    # attention. Against the oracle, then the written slots.
     cfg = dict(ferric_amd.QWEN3_0_6B, layers=2)
     limits = PagedLimits(context_tokens=1024, physical_page_count=3200, page_table_stride=64)
     pair = Pair(cfg, limits, seed=37, rows=32, prefill_rows=128)
     try:
-        rng = np.random.default_rng(37)
-        lengths = [int(x) for x in rng.integers(0, 601, 80)]
+        rng = np.random.default_rng(37 + nseq)
+        lengths = [int(x) for x in rng.integers(0, 601, nseq)]
         sids = pair.admit_with_prefix(lengths)
         rows = [(s, int(t)) for s, t in zip(sids, rng.integers(0, cfg["vocabulary"], len(sids)))]
-        outs = [0, 17, 40, 79]
+        outs = [0, 17, nseq // 2, nseq - 1]
         batch, out, ref = pair.step(rows, outs)
         _mark_written(pair, batch)
-        pair.check(batch, out, ref, "80 one-row blocks")
+        pair.check(batch, out, ref, f"{nseq} one-row blocks")
         pair.check_kv()
     finally:
         pair.close()
